@@ -1,0 +1,23 @@
+"""CPU oracle for the Wan2.2 DiT-block hot path -- TEST INFRASTRUCTURE ONLY.
+
+A restatement, in numpy / torch-on-CPU, of the reference's arithmetic for this path
+(reecedantin/vllm-omni-neuron). Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+CPU-baseline leg may import it, and only as the checker or the reported CPU baseline; the product
+package never imports it and has no CPU fallback.
+
+Modules and what pins each (full table in DESIGN.md):
+
+- ``fp8``: e4m3fn / bf16 rounding and e8m0 scales, bit level. Pinned against torch's own
+  float8_e4m3fn and bfloat16 casts on every bf16 bit pattern plus random fp32 and ties.
+- ``mx``: MX block quantization (shared exponent = block max - 7) and ROW packing. Pinned by
+  known-answer blocks whose codes follow from the rule by hand, and by dequantization bounds.
+- ``adaln``: the canonical fused adaLN (exact fixed-grid statistics). Pinned against
+  ``math.fsum`` sums, ``F.layer_norm`` / eager restatement distance, and LayerNorm invariants.
+- ``rope``: Wan 3D RoPE tables and interleaved rotation. Pinned by norm preservation, the
+  rotate-half equivalence and closed-form angles.
+- ``attention``: exact softmax attention and the constant-max form. Pinned by fp64 brute force,
+  invariance to the subtracted constant, and the underflow clamp.
+- ``gemm``: MXFP8 dequantized fp64 products, GELU-tanh MLP. Pinned by brute-force loops on tiny
+  shapes and closed-form GELU points.
+- ``block``: the Wan transformer block composed from the above (MXFP8 path and BF16 eager path).
+"""

@@ -1,0 +1,42 @@
+"""The C-ABI library loads and exports every entry point include/wanmi.h declares (no GPU calls)."""
+
+import pathlib
+import re
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "wanmi.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wanmi_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "wanmi_adaln_quant" in names and "wanmi_abi_version" in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), f"libwanmi.so does not export {name}"
+    assert set(_declared()) == set(pkg._lib.exported_symbols())
+
+
+def test_abi_version_and_error_reporting(pkg):
+    lib = pkg._lib.load()
+    assert lib.wanmi_abi_version() == 1
+    # an argument error is reported without touching the GPU
+    st = lib.wanmi_adaln_quant(None, None, None, None, None, 4, 100, 1e-6, 1, 1, None, None, None, None)
+    assert st == pkg._lib.WANMI_ERR_ARG
+    assert b"multiple of 32" in lib.wanmi_last_error()
+
+
+def test_cpu_tensor_is_rejected(pkg):
+    import pytest
+    import torch
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.adaln_modulate(x, eps=1e-6)

@@ -1,0 +1,14 @@
+"""MI355X (gfx950) implementation of the Wan2.2-A14B DiT-block hot path.
+
+Drop-ins for the reecedantin/vllm-omni-neuron op boundary of the Wan2.2 transformer block
+(``adaln_modulate``, ``row_mx_qkv_proj``, ``row_mx_mlp``, ``row_mx_o_proj``,
+``wan_cp_self_attention``/``_nki_attend``, ``ring_attention_const_max_fwd``), each backed by
+hand-written HIP kernels in ``libwanmi.so`` and called through its C ABI (``include/wanmi.h``).
+
+The directory name contains dashes, so it is imported under the module name
+``vllm_omni_neuron_amd`` by :func:`__graft_entry__.load_package`.
+"""
+
+from . import _lib  # noqa: F401
+from .adaln_kernels import adaln_modulate  # noqa: F401
+from .common_types import MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401

@@ -1,0 +1,103 @@
+"""ctypes binding of libwanmi.so, the gfx950 kernel library.
+
+There is no CPU fallback: every op in this package runs the HIP kernels or raises. A missing
+library, a CPU tensor, or a non-zero status from the C ABI is an error.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libwanmi.so"
+
+WANMI_OK = 0
+WANMI_ERR_ARG = -1
+WANMI_ERR_UNSUPPORTED = -2
+WANMI_ERR_HIP = -3
+
+NORM = {"none": 0, "layer_norm": 1, "rms_norm": 2}
+QUANT = {"none": 0, "mx": 1, "row": 2}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes, mirroring include/wanmi.h
+_SIGNATURES = {
+    "wanmi_abi_version": [],
+    "wanmi_last_error": [],
+    "wanmi_adaln_quant": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp, _vp, _vp, _vp],
+    "wanmi_e4m3_encode": [_vp, _vp, _i64, _vp],
+}
+
+_LIB = None
+
+
+class WanmiError(RuntimeError):
+    """A HIP launch or runtime failure reported by libwanmi."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libwanmi.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build the gfx950 kernels first (__graft_entry__.build()); "
+            "this package has no CPU fallback"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _i32
+    lib.wanmi_last_error.restype = ctypes.c_char_p
+    _LIB = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(status: int, what: str) -> None:
+    if status == WANMI_OK:
+        return
+    msg = load().wanmi_last_error().decode(errors="replace")
+    if status == WANMI_ERR_ARG:
+        raise ValueError(f"{what}: {msg}")
+    if status == WANMI_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise WanmiError(f"{what}: status {status}: {msg}")
+
+
+def ptr(t: torch.Tensor | None):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    """The current HIP stream of ``t``'s device, as the void* the C ABI takes."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:
+    """Every tensor must live on the same GPU; the kernels never run on the host."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{what}: tensors must be on a ROCm GPU (got {t.device}); no CPU fallback")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise RuntimeError(f"{what}: no tensor given")
+    return dev

@@ -1,0 +1,59 @@
+"""Boundary vocabulary shared by the ops: the reference's enums plus the MX tensor pair.
+
+The enum members mirror vllm_omni_neuron/kernels/nkilib/core/utils/common_types.py (NormType,
+QuantizationType, QKVOutputLayout) so call sites read the same; only the members the Wan DiT
+path uses are kept.
+"""
+
+from __future__ import annotations
+
+import enum
+from typing import NamedTuple
+
+import torch
+
+
+class NormType(enum.Enum):
+    NO_NORM = "none"
+    LAYER_NORM = "layer_norm"
+    RMS_NORM = "rms_norm"
+    RMS_NORM_ACROSS_HEADS = "rms_norm_across_heads"
+
+
+class QuantizationType(enum.Enum):
+    NONE = "none"
+    ROW = "row"
+    MX = "mx"
+    ROW_MX = "row_mx"
+
+
+class QKVOutputLayout(enum.Enum):
+    BSD = "bsd"  # [B, S, (nq + 2 nkv) * d]
+    NBSd = "nbsd"  # [N, B, S, d]
+
+
+class QKNormConfig(NamedTuple):
+    """Across-heads RMSNorm applied to Q and/or K before RoPE (reference QKNormConfig)."""
+
+    q_norm: NormType | None
+    k_norm: NormType | None
+    eps: float = 1e-6
+
+
+class MXTensor(NamedTuple):
+    """An MXFP8 activation: e4m3fn codes [..., K] and one e8m0 scale per 32 codes [..., K/32].
+
+    Element ``i`` of a row dequantizes to ``codes[i] * 2**(scales[i // 32] - 127)``.
+    """
+
+    codes: torch.Tensor  # torch.float8_e4m3fn
+    scales: torch.Tensor  # torch.uint8
+
+    @property
+    def shape(self):
+        return self.codes.shape
+
+    def dequantize(self, dtype=torch.float32) -> torch.Tensor:
+        f = torch.exp2(self.scales.to(torch.float32) - 127.0)
+        f = f.repeat_interleave(32, dim=-1)
+        return (self.codes.to(torch.float32) * f).to(dtype)
