@@ -62,6 +62,31 @@ int wanmi_adaln_quant(const void* hidden, const void* residual, const float* gat
                       const float* add, int64_t T, int64_t H, float eps, int norm_type,
                       int quant_type, void* out, uint8_t* scales, void* residual_out, void* stream);
 
+/* Epilogue selector of wanmi_mxfp8_gemm. */
+#define WANMI_EPI_BF16 0             /* out = bf16(acc * rs * cs + bias) */
+#define WANMI_EPI_GELU_MX 1          /* out, out_scales = MX(bf16(gelu_tanh(acc * rs * cs + bias))) */
+#define WANMI_EPI_GELU_BF16 2        /* out = bf16(gelu_tanh(acc * rs * cs + bias)) */
+#define WANMI_EPI_GATED_RESIDUAL 3   /* out = bf16(residual + bf16(acc * rs * cs + bias) * gate) */
+
+/*
+ * MXFP8 block-scaled GEMM with fused epilogue:
+ *   acc[m,n] = sum_k A[m,k] 2^(a_scales[m,k/32]-127) * W[n,k] 2^(w_scales[n,k/32]-127)   (fp32)
+ * a_codes: e4m3fn [M, lda] (row stride lda >= K, lda % 16 == 0); a_scales: e8m0 [M, K/32];
+ * w_codes: e4m3fn [N, K] (the weight transposed, K-contiguous); w_scales: e8m0 [N, K/32];
+ * row_scale [M], col_scale [N], bias [N], gate [N]: fp32, each optional except as the epilogue
+ * needs (row/col scales give the reference's ROW_MX dequant with neutral 127 block scales);
+ * out: bf16 or e4m3fn [M, ldo]; out_scales: e8m0 [M, N/32] (GELU_MX); residual: bf16 [M, ldo].
+ * Requires N % 256 == 0, K % 128 == 0.
+ * Replaces the ROW_MX projection kernels behind row_mx_qkv_proj / row_mx_o_proj / row_mx_mlp
+ * (vllm_omni_neuron/diffusion/quantization/row_mx_kernels.py:48-198): _qkv_cte_mx_impl
+ * (kernels/nkilib/core/qkv/qkv_cte.py:2725) and mlp_cte_mx (kernels/nkilib/core/mlp/mlp_cte/mx/).
+ */
+int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                     const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                     const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, int epilogue,
+                     void* out, int64_t ldo, uint8_t* out_scales, const void* residual,
+                     const float* gate, void* stream);
+
 /*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,
  * hardware conversion; inputs must satisfy |x| < 464). Test hook for the conversion's known-answer

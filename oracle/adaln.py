@@ -1,20 +1,19 @@
 """Canonical fused adaLN + quantization -- oracle, test infrastructure only.
 
 Restates ``_eager_adaln`` (vllm_omni_neuron/diffusion/quantization/adaln_kernels.py:51-84) with a
-fixed, order-independent definition of the row statistics so that a GPU result can be compared bit
-for bit:
+fixed definition of the row statistics so that a GPU result can be compared bit for bit:
 
     x = h                                     or  x = bf16(fl32(h * gate) + res)   (adaln_kernels.py:58-66)
-    E = max biased fp32 exponent over the row
-    LayerNorm (two-pass, fp64, on an exact fixed grid):
-        S1 = sum rint(x * 2^(165-E)),            mu64  = (S1 * 2^(E-165)) / H
-        S2 = sum rint((x - mu64)^2 * 2^(289-2E)), var64 = (S2 * 2^(2E-289)) / H
-        mu = fp32(mu64), rstd = fp32(1 / sqrt(var64 + eps))
-        xh = fl32(fl32(x - mu) * rstd)
-    RMSNorm: S = sum rint(x^2 * 2^(291-2E)); rrms = fp32(1/sqrt(S*2^(2E-291)/H + eps)); xh = fl32(x*rrms)
+    Summation order (fp32): the row is cut into chunks of 512 columns; "lane" l (0..63) owns
+    columns c*512 + 8l .. 8l+7 of every chunk c and adds its values sequentially (chunk by chunk,
+    column order inside a chunk); the 64 lane sums then combine in an xor butterfly with offsets
+    32, 16, 8, 4, 2, 1 (v_l <- v_l + v_(l^o)).
+    LayerNorm (two-pass): mu = S1 / H,  S1 = sum x
+                          var = S2 / H, S2 = sum fl(fl(x - mu)^2),  rstd = fp32(1/sqrt(fp64(var) + eps))
+                          xh = fl32(fl32(x - mu) * rstd)
+    RMSNorm:  ms = S / H, S = sum fl(x^2), rrms = fp32(1/sqrt(fp64(ms) + eps)), xh = fl32(x * rrms)
     y = bf16(fl32(fl32(xh * mul) + add))      (mul / add optional, fp32, no FMA)
 
-Every rounded term is an integer of magnitude < 2^39 and H <= 16384, so each sum is exact in fp64.
 ``F.layer_norm``'s own fp32 reduction order is not reproducible off the CPU it ran on; the distance
 from this definition to the eager path is measured in the tests (bf16 ulps of y).
 """
@@ -29,32 +28,51 @@ from . import mx as mx_mod
 from .fp8 import bf16_round, exp_field
 
 
-def _row_exp_max(x: np.ndarray) -> np.ndarray:
-    return exp_field(x).max(axis=-1, keepdims=True)
+def _lane_major(x: np.ndarray) -> np.ndarray:
+    """[T, H] -> [T, 64, NCH*8]: each lane's columns in its summation order (zero padded)."""
+    T, H = x.shape
+    nch = -(-H // 512)
+    xp = np.zeros((T, nch * 512), np.float32)
+    xp[:, :H] = x
+    return xp.reshape(T, nch, 64, 8).transpose(0, 2, 1, 3).reshape(T, 64, nch * 8)
+
+
+def _valid_lane_major(T: int, H: int) -> np.ndarray:
+    return _lane_major(np.ones((1, H), np.float32))[0] > 0
+
+
+def _ordered_sum(terms: np.ndarray) -> np.ndarray:
+    """[T, 64, n] fp32 -> [T, 1]: sequential per-lane fp32 sums, then the xor butterfly."""
+    acc = np.zeros(terms.shape[:2], np.float32)
+    for i in range(terms.shape[2]):
+        acc = (acc + terms[:, :, i]).astype(np.float32)
+    lanes = np.arange(64)
+    for o in (32, 16, 8, 4, 2, 1):
+        acc = (acc + acc[:, lanes ^ o]).astype(np.float32)
+    return acc[:, :1]
 
 
 def layer_norm_stats(x: np.ndarray, eps: float):
-    """x fp32 [..., H] -> (mu fp32 [..., 1], rstd fp32 [..., 1]) per the fixed-grid definition."""
-    H = x.shape[-1]
-    E = _row_exp_max(x)
-    xd = x.astype(np.float64)
-    s1 = np.rint(np.ldexp(xd, 165 - E)).sum(axis=-1, keepdims=True)
-    mu64 = np.ldexp(s1, E - 165) / np.float64(H)
-    d = xd - mu64
-    s2 = np.rint(np.ldexp(d * d, 289 - 2 * E)).sum(axis=-1, keepdims=True)
-    var64 = np.ldexp(s2, 2 * E - 289) / np.float64(H)
-    rstd64 = 1.0 / np.sqrt(var64 + np.float64(np.float32(eps)))
-    return mu64.astype(np.float32), rstd64.astype(np.float32)
+    """x fp32 [T, H] -> (mu fp32 [T, 1], rstd fp32 [T, 1]) in the canonical order."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, x.shape[-1])
+    T, H = x.shape
+    lm = _lane_major(x)
+    mu = (_ordered_sum(lm) / np.float32(H)).astype(np.float32)
+    d = (lm - mu[:, :, None]).astype(np.float32)
+    q = (d * d).astype(np.float32)
+    q = np.where(_valid_lane_major(T, H)[None], q, np.float32(0.0))
+    var = (_ordered_sum(q) / np.float32(H)).astype(np.float32)
+    rstd = (1.0 / np.sqrt(var.astype(np.float64) + np.float64(np.float32(eps)))).astype(np.float32)
+    return mu, rstd
 
 
 def rms_norm_stat(x: np.ndarray, eps: float) -> np.ndarray:
-    """x fp32 [..., H] -> rrms fp32 [..., 1]."""
+    """x fp32 [T, H] -> rrms fp32 [T, 1] in the canonical order."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, x.shape[-1])
     H = x.shape[-1]
-    E = _row_exp_max(x)
-    xd = x.astype(np.float64)
-    s = np.rint(np.ldexp(xd * xd, 291 - 2 * E)).sum(axis=-1, keepdims=True)
-    ms64 = np.ldexp(s, 2 * E - 291) / np.float64(H)
-    return (1.0 / np.sqrt(ms64 + np.float64(np.float32(eps)))).astype(np.float32)
+    lm = _lane_major(x)
+    ms = (_ordered_sum((lm * lm).astype(np.float32)) / np.float32(H)).astype(np.float32)
+    return (1.0 / np.sqrt(ms.astype(np.float64) + np.float64(np.float32(eps)))).astype(np.float32)
 
 
 def adaln_y(hidden, mul=None, add=None, *, eps=1e-6, norm_type="layer_norm", residual=None, gate=None):
@@ -62,7 +80,10 @@ def adaln_y(hidden, mul=None, add=None, *, eps=1e-6, norm_type="layer_norm", res
 
     hidden / residual: fp32 arrays holding bf16 values, [..., H]; mul / add / gate: fp32 [H] or None.
     """
-    x = np.ascontiguousarray(hidden, dtype=np.float32)
+    shape = np.shape(hidden)
+    x = np.ascontiguousarray(hidden, dtype=np.float32).reshape(-1, shape[-1])
+    if residual is not None:
+        residual = np.asarray(residual, np.float32).reshape(-1, shape[-1])
     res_out = None
     if residual is not None:
         if gate is not None:
@@ -84,7 +105,8 @@ def adaln_y(hidden, mul=None, add=None, *, eps=1e-6, norm_type="layer_norm", res
         t = (t * np.asarray(mul, np.float32)).astype(np.float32)
     if add is not None:
         t = (t + np.asarray(add, np.float32)).astype(np.float32)
-    return bf16_round(t), res_out
+    y = bf16_round(t).reshape(shape)
+    return y, (None if res_out is None else res_out.reshape(shape))
 
 
 def adaln_quant(hidden, mul=None, add=None, *, eps=1e-6, norm_type="layer_norm", quant="none",

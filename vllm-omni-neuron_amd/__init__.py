@@ -12,3 +12,4 @@ The directory name contains dashes, so it is imported under the module name
 from . import _lib  # noqa: F401
 from .adaln_kernels import adaln_modulate  # noqa: F401
 from .common_types import MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401
+from .row_mx_kernels import MXWeight, mxfp8_linear, quantize_weight_mx, row_mx_mlp  # noqa: F401

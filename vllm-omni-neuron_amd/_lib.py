@@ -32,6 +32,7 @@ _SIGNATURES = {
     "wanmi_last_error": [],
     "wanmi_adaln_quant": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp, _vp, _vp, _vp],
     "wanmi_e4m3_encode": [_vp, _vp, _i64, _vp],
+    "wanmi_mxfp8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp],
 }
 
 _LIB = None

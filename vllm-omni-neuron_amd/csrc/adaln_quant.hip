@@ -4,16 +4,17 @@
 // c < ceil(H/512), so every load and store is a 16-byte (or 8-byte) access and one chunk of a wave
 // is a contiguous 1 KiB (512 B for codes) span of the row. The row makes exactly one HBM round trip.
 //
-// Statistics are exact: each element is rounded once onto a fixed power-of-two grid chosen from
-// the row's largest exponent E, so every partial sum is an integer below 2^53 and fp64 adds it
-// without error in any order. The result therefore does not depend on how lanes or waves combine,
-// and the CPU oracle reproduces it bit for bit with plain numpy.
+// Statistics use a fixed summation order so the CPU oracle reproduces them bit for bit: every lane
+// sums its own columns sequentially in fp32 (chunk by chunk, column order within a chunk), then the
+// 64 lane sums combine in an xor butterfly (offsets 32, 16, 8, 4, 2, 1). Two passes:
 //
-//   LayerNorm: S1 = sum rint(x * 2^(165-E));          mu  = (S1 * 2^(E-165)) / H       (fp64)
-//              S2 = sum rint((x-mu)^2 * 2^(289-2E));  var = (S2 * 2^(2E-289)) / H
-//              rstd = 1 / sqrt(var + eps)  (fp64), then mu, rstd rounded to fp32
-//   RMSNorm:   S  = sum rint(x^2 * 2^(291-2E));        rrms = 1 / sqrt(S*2^(2E-291)/H + eps)
+//   LayerNorm: mu = S1 / H with S1 = sum x;  var = S2 / H with S2 = sum fl(fl(x - mu)^2)   (fp32)
+//              rstd = fp32(1 / sqrt(fp64(var) + eps))
+//   RMSNorm:   ms = S / H with S = sum fl(x^2);  rrms = fp32(1 / sqrt(fp64(ms) + eps))
 //   y = bf16( ((x - mu) * rstd) * mul + add )         (fp32, each op rounded, no FMA)
+//
+// That is ~4 VALU ops per element for the statistics, which keeps the pass memory-bound: at 8 TB/s
+// and 3 bytes moved per element there are only ~15 VALU ops per element to spend.
 //
 // Semantics follow _eager_adaln (vllm_omni_neuron/diffusion/quantization/adaln_kernels.py:51-84):
 // gated residual add in fp32 then a bf16 round, normalization in fp32, modulation by fp32 mul/add,
@@ -40,231 +41,229 @@ struct AdalnArgs {
   uint16_t* residual_out;
 };
 
-// Exponent field of a bf16 held in the low / high half of a packed pair.
-__device__ __forceinline__ int bexp_lo(uint32_t u) { return (int)((u >> 7) & 0xFFu); }
-__device__ __forceinline__ int bexp_hi(uint32_t u) { return (int)((u >> 23) & 0xFFu); }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer descriptor word 3
 
+// A buffer descriptor over `bytes` bytes at `p`; accesses past the end read 0 / are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c, float (&v)[8]) {
+  const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 32, c * 2048, 0);
+  const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 32 + 16, c * 2048, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = __uint_as_float(v0[j]);
+    v[4 + j] = __uint_as_float(v1[j]);
+  }
+}
+
+// Each tensor is addressed through a buffer descriptor based at the current row (scalar registers),
+// one per-lane byte offset and the chunk offset in the scalar soffset field, so no per-chunk vector
+// address is ever materialized; descriptor extents mask the columns past H in a partial chunk.
 template <int NCH>
-__global__ __launch_bounds__(256) void adaln_quant_kernel(AdalnArgs a) {
+__global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.H;
   const int nch = a.nch;
-  const int64_t row_stride_waves = (int64_t)gridDim.x * 4;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= a.T) return;
+  const int64_t rbase = row * (int64_t)H;
 
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < a.T; row += row_stride_waves) {
-    uint32_t xp[NCH][4];  // the row's x as packed bf16 pairs (exact; also the residual sum)
-    const int64_t rbase = row * (int64_t)H;
+  const __amdgpu_buffer_rsrc_t r_x = rsrc(a.hidden + rbase, 2 * (int64_t)H);
+  uint32_t xp[NCH][4];  // the row's x as packed bf16 pairs (exact; also the residual sum)
 
-    // ---- load (and optional gated residual add) ----
+  // ---- load (and optional gated residual add, x = bf16(h * gate + res)) ----
+  if (a.residual) {
+    const __amdgpu_buffer_rsrc_t r_r = rsrc(a.residual + rbase, 2 * (int64_t)H);
+    const __amdgpu_buffer_rsrc_t r_ro = rsrc(a.residual_out + rbase, 2 * (int64_t)H);
+    const __amdgpu_buffer_rsrc_t r_g = rsrc(a.gate, 4 * (int64_t)H);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int col = c * 512 + lane * 8;
-      const bool ok = (c < nch) && (col < H);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (ok) {
-        v = *reinterpret_cast<const uint4*>(a.hidden + rbase + col);
-        if (a.residual) {
-          const uint4 r = *reinterpret_cast<const uint4*>(a.residual + rbase + col);
-          const uint32_t hv[4] = {v.x, v.y, v.z, v.w};
-          const uint32_t rv[4] = {r.x, r.y, r.z, r.w};
-          float gv[8];
+      if (c < nch) {
+        const u32x4 hv = __builtin_amdgcn_raw_buffer_load_b128(r_x, lane * 16, c * 1024, 0);
+        const u32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(r_r, lane * 16, c * 1024, 0);
+        float gv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        if (a.gate) load8f(r_g, lane, c, gv);
+        u32x4 ov;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float h0 = bf16_lo(hv[j]), h1 = bf16_hi(hv[j]);
           if (a.gate) {
-            const float4 g0 = *reinterpret_cast<const float4*>(a.gate + col);
-            const float4 g1 = *reinterpret_cast<const float4*>(a.gate + col + 4);
-            gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
-            gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+            h0 = h0 * gv[2 * j];
+            h1 = h1 * gv[2 * j + 1];
           }
-          uint32_t ov[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float h0 = bf16_lo(hv[j]), h1 = bf16_hi(hv[j]);
-            if (a.gate) {
-              h0 = h0 * gv[2 * j];
-              h1 = h1 * gv[2 * j + 1];
-            }
-            const float s0 = h0 + bf16_lo(rv[j]);
-            const float s1 = h1 + bf16_hi(rv[j]);
-            ov[j] = pack_bf16x2(s0, s1);
-          }
-          v = make_uint4(ov[0], ov[1], ov[2], ov[3]);
-          *reinterpret_cast<uint4*>(a.residual_out + rbase + col) = v;
+          ov[j] = pack_bf16x2(h0 + bf16_lo(rv[j]), h1 + bf16_hi(rv[j]));
+          xp[c][j] = ov[j];
         }
-      }
-      xp[c][0] = v.x;
-      xp[c][1] = v.y;
-      xp[c][2] = v.z;
-      xp[c][3] = v.w;
-    }
-
-    // ---- statistics ----
-    float mu = 0.0f, rs = 1.0f;
-    if (a.norm != WANMI_NORM_NONE) {
-      int e = 0;
+        __builtin_amdgcn_raw_buffer_store_b128(ov, r_ro, lane * 16, c * 1024, 0);
+      } else {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) e = max(e, max(bexp_lo(xp[c][j]), bexp_hi(xp[c][j])));
-      const int E = wave_max_i32(e);
-      const double deps = (double)a.eps;
-      if (a.norm == WANMI_NORM_LAYER) {
-        double s1 = 0.0;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            s1 += rint(ldexp((double)bf16_lo(xp[c][j]), 165 - E));
-            s1 += rint(ldexp((double)bf16_hi(xp[c][j]), 165 - E));
-          }
-        s1 = wave_sum_f64(s1);
-        const double mu64 = ldexp(s1, E - 165) / (double)H;
-        double s2 = 0.0;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const bool ok = (c < nch) && (c * 512 + lane * 8 < H);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const double d0 = (double)bf16_lo(xp[c][j]) - mu64;
-            const double d1 = (double)bf16_hi(xp[c][j]) - mu64;
-            const double q0 = rint(ldexp(d0 * d0, 289 - 2 * E));
-            const double q1 = rint(ldexp(d1 * d1, 289 - 2 * E));
-            s2 += ok ? q0 : 0.0;
-            s2 += ok ? q1 : 0.0;
-          }
-        }
-        s2 = wave_sum_f64(s2);
-        const double var64 = ldexp(s2, 2 * E - 289) / (double)H;
-        const double rstd64 = 1.0 / sqrt(var64 + deps);
-        mu = (float)mu64;
-        rs = (float)rstd64;
-      } else {  // RMS
-        double s = 0.0;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const double v0 = (double)bf16_lo(xp[c][j]);
-            const double v1 = (double)bf16_hi(xp[c][j]);
-            s += rint(ldexp(v0 * v0, 291 - 2 * E));
-            s += rint(ldexp(v1 * v1, 291 - 2 * E));
-          }
-        s = wave_sum_f64(s);
-        const double ms64 = ldexp(s, 2 * E - 291) / (double)H;
-        rs = (float)(1.0 / sqrt(ms64 + deps));
+        for (int j = 0; j < 4; ++j) xp[c][j] = 0u;
       }
     }
-
-    // ---- normalize + modulate: y = bf16(((x - mu) * rs) * mul + add), in place in xp ----
+  } else {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int col = c * 512 + lane * 8;
-      const bool ok = (c < nch) && (col < H);
-      float mv[8], av[8];
-      if (ok && a.mul) {
-        const float4 m0 = *reinterpret_cast<const float4*>(a.mul + col);
-        const float4 m1 = *reinterpret_cast<const float4*>(a.mul + col + 4);
-        mv[0] = m0.x; mv[1] = m0.y; mv[2] = m0.z; mv[3] = m0.w;
-        mv[4] = m1.x; mv[5] = m1.y; mv[6] = m1.z; mv[7] = m1.w;
+      if (c < nch) {
+        const u32x4 hv = __builtin_amdgcn_raw_buffer_load_b128(r_x, lane * 16, c * 1024, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[c][j] = hv[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[c][j] = 0u;
       }
-      if (ok && a.add) {
-        const float4 b0 = *reinterpret_cast<const float4*>(a.add + col);
-        const float4 b1 = *reinterpret_cast<const float4*>(a.add + col + 4);
-        av[0] = b0.x; av[1] = b0.y; av[2] = b0.z; av[3] = b0.w;
-        av[4] = b1.x; av[5] = b1.y; av[6] = b1.z; av[7] = b1.w;
-      }
+    }
+  }
+  // Columns past H were read as zero through the descriptor extent.
+
+  // ---- statistics (fixed-order fp32 sums, see the file header) ----
+  float mu = 0.0f, rs = 1.0f;
+  if (a.norm == WANMI_NORM_LAYER) {
+    float s1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (!ok) {  // columns past H stay zero so row-wide reductions below ignore them
-          xp[c][j] = 0u;
-          continue;
-        }
-        float v0 = bf16_lo(xp[c][j]), v1 = bf16_hi(xp[c][j]);
-        if (a.norm == WANMI_NORM_LAYER) {
-          v0 = (v0 - mu) * rs;
-          v1 = (v1 - mu) * rs;
-        } else if (a.norm == WANMI_NORM_RMS) {
-          v0 = v0 * rs;
-          v1 = v1 * rs;
-        }
-        if (a.mul) {
-          v0 = v0 * mv[2 * j];
-          v1 = v1 * mv[2 * j + 1];
-        }
-        if (a.add) {
-          v0 = v0 + av[2 * j];
-          v1 = v1 + av[2 * j + 1];
-        }
-        xp[c][j] = pack_bf16x2(v0, v1);
+        s1 = s1 + bf16_lo(xp[c][j]);
+        s1 = s1 + bf16_hi(xp[c][j]);
+      }
+    s1 = wave_sum_f32(s1);
+    mu = s1 / (float)H;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const bool ok = (c < nch) && (c * 512 + lane * 8 < H);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d0 = bf16_lo(xp[c][j]) - mu;
+        const float d1 = bf16_hi(xp[c][j]) - mu;
+        const float q0 = d0 * d0;
+        const float q1 = d1 * d1;
+        s2 = s2 + (ok ? q0 : 0.0f);
+        s2 = s2 + (ok ? q1 : 0.0f);
       }
     }
-
-    // ---- quantize + store ----
-    if (a.quant == WANMI_QUANT_NONE) {
-      uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+    s2 = wave_sum_f32(s2);
+    const float var = s2 / (float)H;
+    rs = (float)(1.0 / sqrt((double)var + (double)a.eps));
+  } else if (a.norm == WANMI_NORM_RMS) {
+    float s = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int col = c * 512 + lane * 8;
-        if ((c < nch) && (col < H))
-          *reinterpret_cast<uint4*>(out + rbase + col) = make_uint4(xp[c][0], xp[c][1], xp[c][2], xp[c][3]);
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = bf16_lo(xp[c][j]);
+        const float v1 = bf16_hi(xp[c][j]);
+        const float q0 = v0 * v0;
+        const float q1 = v1 * v1;
+        s = s + q0;
+        s = s + q1;
       }
-    } else if (a.quant == WANMI_QUANT_MX) {
-      uint8_t* codes = reinterpret_cast<uint8_t*>(a.out);
-      const int64_t sbase = row * (int64_t)(H / 32);
+    s = wave_sum_f32(s);
+    const float ms = s / (float)H;
+    rs = (float)(1.0 / sqrt((double)ms + (double)a.eps));
+  }
+
+  // Keep the per-chunk mul/add loads below the statistics: hoisted above them, all chunks' vectors
+  // would be live at once (8 floats x 2 x NCH per lane) and halve occupancy.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- normalize + modulate (+ quantize + store), one chunk at a time ----
+  // y = bf16(((x - mu) * rs) * mul + add). NONE and MX finish each chunk here; ROW keeps y in xp
+  // for a second pass because its scale needs the whole row's max.
+  const __amdgpu_buffer_rsrc_t r_m = rsrc(a.mul, 4 * (int64_t)H);
+  const __amdgpu_buffer_rsrc_t r_a = rsrc(a.add, 4 * (int64_t)H);
+  const int64_t out_row_bytes = a.quant == WANMI_QUANT_NONE ? 2 * (int64_t)H
+                                : a.quant == WANMI_QUANT_MX  ? (int64_t)H
+                                                             : (int64_t)H + 4;
+  const __amdgpu_buffer_rsrc_t r_o =
+      rsrc(reinterpret_cast<const uint8_t*>(a.out) + row * out_row_bytes, out_row_bytes);
+  float amax = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        if (c >= nch) break;  // uniform across the wave
-        const int col = c * 512 + lane * 8;
+  for (int c = 0; c < NCH; ++c) {
+    if (c < nch) {
+      const bool ok = c * 512 + lane * 8 < H;
+      float y[8];
+      {
+        float mv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        float av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (a.mul) load8f(r_m, lane, c, mv);
+        if (a.add) load8f(r_a, lane, c, av);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float v = (j & 1) ? bf16_hi(xp[c][j >> 1]) : bf16_lo(xp[c][j >> 1]);
+          if (a.norm == WANMI_NORM_LAYER) {
+            v = (v - mu) * rs;
+          } else if (a.norm == WANMI_NORM_RMS) {
+            v = v * rs;
+          }
+          if (a.mul) v = v * mv[j];
+          if (a.add) v = v + av[j];
+          y[j] = ok ? round_bf16(v) : 0.0f;  // columns past H stay zero for the row reductions
+        }
+      }
+      if (a.quant == WANMI_QUANT_NONE) {
+        u32x4 ov;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ov[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
+        __builtin_amdgcn_raw_buffer_store_b128(ov, r_o, lane * 16, c * 1024, 0);
+      } else if (a.quant == WANMI_QUANT_MX) {
+        // a 32-block is 4 consecutive lanes (col / 32 == c * 16 + lane / 4)
         int e = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e = max(e, max(bexp_lo(xp[c][j]), bexp_hi(xp[c][j])));
+        for (int j = 0; j < 8; ++j) e = max(e, exp_field(y[j]));
         e = max(e, __shfl_xor(e, 1, 64));
         e = max(e, __shfl_xor(e, 2, 64));
-        const int s = max(e - 7, 0);
-        const float f = mx_inv_scale(s);
-        const uint32_t lo = cvt_e4m3x4(bf16_lo(xp[c][0]) * f, bf16_hi(xp[c][0]) * f,
-                                       bf16_lo(xp[c][1]) * f, bf16_hi(xp[c][1]) * f);
-        const uint32_t hi = cvt_e4m3x4(bf16_lo(xp[c][2]) * f, bf16_hi(xp[c][2]) * f,
-                                       bf16_lo(xp[c][3]) * f, bf16_hi(xp[c][3]) * f);
-        if (col < H) {
-          *reinterpret_cast<uint2*>(codes + rbase + col) = make_uint2(lo, hi);
-          if ((lane & 3) == 0) a.scales[sbase + col / 32] = (uint8_t)s;
-        }
+        const int sexp = max(e - 7, 0);
+        const float f = mx_inv_scale(sexp);
+        u32x2 cv;
+        cv[0] = cvt_e4m3x4(y[0] * f, y[1] * f, y[2] * f, y[3] * f);
+        cv[1] = cvt_e4m3x4(y[4] * f, y[5] * f, y[6] * f, y[7] * f);
+        __builtin_amdgcn_raw_buffer_store_b64(cv, r_o, lane * 8, c * 512, 0);
+        if (ok && (lane & 3) == 0) a.scales[row * (int64_t)(H / 32) + c * 16 + (lane >> 2)] = (uint8_t)sexp;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(y[j]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[c][j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
       }
-    } else {  // ROW: codes = e4m3(y / dq), dq = max(amax / 448, 1e-6), fp32 dq appended
-      float amax = 0.0f;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(xp[c][j])), fabsf(bf16_hi(xp[c][j]))));
-      amax = wave_max_f32(amax);
-      const float dq = fmaxf(amax / 448.0f, 1e-6f);
-      uint8_t* prow = reinterpret_cast<uint8_t*>(a.out) + row * (int64_t)(H + 4);
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int col = c * 512 + lane * 8;
-        if ((c < nch) && (col < H)) {
-          float q[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            q[2 * j] = fminf(fmaxf(bf16_lo(xp[c][j]) / dq, -448.0f), 448.0f);
-            q[2 * j + 1] = fminf(fmaxf(bf16_hi(xp[c][j]) / dq, -448.0f), 448.0f);
-          }
-          uint32_t* dst = reinterpret_cast<uint32_t*>(prow + col);
-          dst[0] = cvt_e4m3x4(q[0], q[1], q[2], q[3]);
-          dst[1] = cvt_e4m3x4(q[4], q[5], q[6], q[7]);
-        }
-      }
-      if (lane == 0) *reinterpret_cast<float*>(prow + H) = dq;
     }
+  }
+
+  // ---- ROW: codes = e4m3(y / dq), dq = max(amax / 448, 1e-6), fp32 dq appended ----
+  if (a.quant == WANMI_QUANT_ROW) {
+    amax = wave_max_f32(amax);
+    const float dq = fmaxf(amax / 448.0f, 1e-6f);
+    // The packed row is H + 4 bytes: codes through a descriptor over H bytes, then the scale.
+    const __amdgpu_buffer_rsrc_t r_c =
+        rsrc(reinterpret_cast<const uint8_t*>(a.out) + row * out_row_bytes, (int64_t)H);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c < nch) {
+        float q[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          q[2 * j] = fminf(fmaxf(bf16_lo(xp[c][j]) / dq, -448.0f), 448.0f);
+          q[2 * j + 1] = fminf(fmaxf(bf16_hi(xp[c][j]) / dq, -448.0f), 448.0f);
+        }
+        u32x2 cv;
+        cv[0] = cvt_e4m3x4(q[0], q[1], q[2], q[3]);
+        cv[1] = cvt_e4m3x4(q[4], q[5], q[6], q[7]);
+        __builtin_amdgcn_raw_buffer_store_b64(cv, r_c, lane * 8, c * 512, 0);
+      }
+    }
+    if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dq), r_o, H, 0, 0);
   }
 }
 
 template <int NCH>
 static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
-  int64_t blocks = (a.T + 3) / 4;
-  if (blocks > 1048576) blocks = 1048576;  // grid-stride loop covers the rest
+  const int64_t blocks = (a.T + 3) / 4;
   hipLaunchKernelGGL(adaln_quant_kernel<NCH>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
@@ -281,6 +280,7 @@ extern "C" int wanmi_adaln_quant(const void* hidden, const void* residual, const
                 "wanmi_adaln_quant: H=%lld must be a positive multiple of 32", (long long)H);
   WANMI_REQUIRE(H <= 16384, WANMI_ERR_UNSUPPORTED, "wanmi_adaln_quant: H=%lld exceeds 16384",
                 (long long)H);
+  WANMI_REQUIRE(T < (1LL << 33), WANMI_ERR_ARG, "wanmi_adaln_quant: T=%lld too large", (long long)T);
   WANMI_REQUIRE(norm_type == WANMI_NORM_NONE || norm_type == WANMI_NORM_LAYER ||
                     norm_type == WANMI_NORM_RMS,
                 WANMI_ERR_ARG, "wanmi_adaln_quant: unknown norm_type %d", norm_type);

@@ -44,16 +44,14 @@ __device__ __forceinline__ float bf16_lo(uint32_t packed) { return __uint_as_flo
 __device__ __forceinline__ float bf16_hi(uint32_t packed) { return __uint_as_float(packed & 0xFFFF0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN is not produced by these kernels).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
-}
-__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+// fp32 -> bf16, round to nearest even, via the gfx950 packed converter (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+__device__ __forceinline__ float round_bf16(float f) { return bf16_lo(pack_bf16x2(f, 0.0f)); }
 
 // Biased fp32 exponent field of |f| (0 for zeros and subnormals), the MX block-max input.
 __device__ __forceinline__ int exp_field(float f) { return (int)((__float_as_uint(f) >> 23) & 0xFFu); }
@@ -81,6 +79,12 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Butterfly sum, offsets 32, 16, 8, 4, 2, 1: every lane ends with the same fp32 value (adds commute).
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
   return v;
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {

@@ -1,0 +1,177 @@
+"""MXFP8 projection entry points for the Wan DiT on gfx950.
+
+Drop-ins for the reference's ROW_MX projection launchers
+(vllm_omni_neuron/diffusion/quantization/row_mx_kernels.py):
+
+- :func:`row_mx_mlp` (row_mx_kernels.py:141-198): gate-less GELU-tanh MLP, up projection with the
+  GELU + MX re-quantization fused in its epilogue, then the down projection.
+- :func:`row_mx_qkv_proj` (row_mx_kernels.py:48-111) and :func:`row_mx_o_proj` (114-138) are in
+  :mod:`.attention_ops` next to the Q/K normalization they fuse with.
+
+Weights live in the GEMM's own layout, an :class:`MXWeight`: the reference-layout ``[K, N]``
+weight (``x @ W``) transposed to ``[N, K]`` and MX-quantized along K (one e8m0 scale per 32),
+produced once by :func:`quantize_weight_mx` -- the counterpart of the reference's offline weight
+packers (row_mx_loaders.py), which lay FP8 weights out for Neuron SBUF instead.
+
+Activations are :class:`MXTensor` (what ``adaln_modulate(quant="mx")`` returns) or the reference's
+packed ROW layout ``[..., K + 4]``; the latter is split into codes, neutral block scales and a
+per-row fp32 scale applied in the epilogue (ROW_MX semantics, qkv_cte.py:3996-4021).
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+from .adaln_kernels import adaln_quant_2d
+from .common_types import MXTensor
+
+EPILOGUES = {"bf16": 0, "gelu_mx": 1, "gelu_bf16": 2, "gated_residual": 3}
+_NEUTRAL_SCALE = 127
+
+
+class MXWeight(NamedTuple):
+    """A projection weight in GEMM layout: ``codes [N, K]`` e4m3fn, ``scales [N, K/32]`` e8m0,
+    an optional per-output-channel fp32 ``col_scale [N]`` (ROW_MX dequant) and fp32 ``bias [N]``."""
+
+    codes: torch.Tensor
+    scales: torch.Tensor
+    col_scale: torch.Tensor | None = None
+    bias: torch.Tensor | None = None
+
+    @property
+    def out_features(self) -> int:
+        return self.codes.shape[0]
+
+    @property
+    def in_features(self) -> int:
+        return self.codes.shape[1]
+
+
+def quantize_weight_mx(weight_kn: torch.Tensor, bias: torch.Tensor | None = None) -> MXWeight:
+    """Reference-layout weight ``[K, N]`` (bf16, on the GPU) -> :class:`MXWeight` ``[N, K]``.
+
+    The transpose is a one-time layout change; the quantization runs the adaLN kernel with no
+    normalization and MX output, i.e. exactly the activation quantizer, along K.
+    """
+    if weight_kn.dim() != 2:
+        raise ValueError("weight must be [K, N]")
+    wt = weight_kn.to(torch.bfloat16).t().contiguous()
+    q = adaln_quant_2d(wt, None, None, eps=0.0, norm_type="none", quant="mx")
+    b = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
+    return MXWeight(q.codes, q.scales, None, b)
+
+
+def _split_row_packed(packed: torch.Tensor):
+    """Reference ROW-packed ``[T, K + 4]`` -> (codes [T, K], neutral scales, row scale [T])."""
+    raw = packed.view(torch.uint8)
+    K = raw.shape[-1] - 4
+    codes = raw[:, :K].contiguous()
+    row_scale = raw[:, K:].contiguous().view(torch.float32).reshape(-1)
+    scales = torch.full((raw.shape[0], K // 32), _NEUTRAL_SCALE, dtype=torch.uint8, device=raw.device)
+    return codes, scales, row_scale
+
+
+def _as_mx_2d(x):
+    """MXTensor / ROW-packed tensor of any leading shape -> (codes2d, scales2d, row_scale, lead)."""
+    if isinstance(x, MXTensor):
+        K = x.codes.shape[-1]
+        lead = x.codes.shape[:-1]
+        codes = x.codes.reshape(-1, K).view(torch.uint8)
+        scales = x.scales.reshape(-1, K // 32)
+        return codes, scales, None, lead
+    lead = x.shape[:-1]
+    codes, scales, row_scale = _split_row_packed(x.reshape(-1, x.shape[-1]))
+    return codes, scales, row_scale, lead
+
+
+def mxfp8_linear(
+    x,
+    weight: MXWeight,
+    *,
+    epilogue: str = "bf16",
+    residual: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+):
+    """``epilogue(x @ W^T * row_scale * col_scale + bias)`` on the MXFP8 GEMM kernel.
+
+    ``x``: :class:`MXTensor` ``[..., K]`` or ROW-packed ``[..., K + 4]``. Returns bf16 ``[..., N]``,
+    or an :class:`MXTensor` for ``epilogue="gelu_mx"``. ``gated_residual`` computes
+    ``bf16(residual + bf16(y) * gate)`` with ``residual`` bf16 ``[..., N]`` and ``gate`` fp32 ``[N]``.
+    """
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"unknown epilogue {epilogue!r}")
+    lib = _lib.load()
+    codes, scales, row_scale, lead = _as_mx_2d(x)
+    M, K = codes.shape
+    N = weight.out_features
+    if weight.in_features != K:
+        raise ValueError(f"activation K={K} does not match weight K={weight.in_features}")
+    _lib.require_gpu(codes, weight.codes, residual, gate, what="mxfp8_linear")
+    dev = codes.device
+    out_scales = None
+    if epilogue == "gelu_mx":
+        out = torch.empty((M, N), dtype=torch.uint8, device=dev) if out is None else out
+        out_scales = torch.empty((M, N // 32), dtype=torch.uint8, device=dev)
+    else:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if out is None else out
+    res2 = None
+    if epilogue == "gated_residual":
+        if residual is None or gate is None:
+            raise ValueError("gated_residual needs residual and gate")
+        res2 = residual.reshape(M, N).contiguous()
+        gate = gate.reshape(N).to(torch.float32).contiguous()
+    status = lib.wanmi_mxfp8_gemm(
+        _lib.ptr(codes),
+        _lib.ptr(scales),
+        _lib.ptr(weight.codes),
+        _lib.ptr(weight.scales),
+        _lib.ptr(row_scale),
+        _lib.ptr(weight.col_scale),
+        _lib.ptr(weight.bias),
+        M,
+        N,
+        K,
+        codes.stride(0),
+        EPILOGUES[epilogue],
+        _lib.ptr(out),
+        out.stride(0),
+        _lib.ptr(out_scales),
+        _lib.ptr(res2),
+        _lib.ptr(gate if epilogue == "gated_residual" else None),
+        _lib.stream_of(codes),
+    )
+    _lib.check(status, "wanmi_mxfp8_gemm")
+    if epilogue == "gelu_mx":
+        return MXTensor(out.view(torch.float8_e4m3fn).reshape(*lead, N), out_scales.reshape(*lead, N // 32))
+    return out.reshape(*lead, N)
+
+
+def row_mx_mlp(
+    packed_hidden,
+    up_weight: MXWeight,
+    down_weight: MXWeight,
+    up_w_scale: torch.Tensor | None = None,
+    down_w_scale: torch.Tensor | None = None,
+    up_bias: torch.Tensor | None = None,
+    down_bias: torch.Tensor | None = None,
+):
+    """Wan's gate-less GELU-tanh MLP: ``down(MX(GELU_tanh(up(x) + b_up))) + b_down``.
+
+    Same argument order as the reference (row_mx_kernels.py:141-149). ``*_w_scale`` are optional
+    per-output-channel fp32 dequant scales (the ROW_MX recipe); biases override the weights' own.
+    Returns bf16 ``[..., H]``.
+    """
+    up = _with(up_weight, up_w_scale, up_bias)
+    down = _with(down_weight, down_w_scale, down_bias)
+    inter = mxfp8_linear(packed_hidden, up, epilogue="gelu_mx")
+    return mxfp8_linear(inter, down, epilogue="bf16")
+
+
+def _with(w: MXWeight, col_scale, bias) -> MXWeight:
+    cs = w.col_scale if col_scale is None else col_scale.reshape(-1).to(torch.float32).contiguous()
+    b = w.bias if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
+    return MXWeight(w.codes, w.scales, cs, b)
