@@ -88,6 +88,62 @@ int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales, const uint
                      const float* gate, void* stream);
 
 /*
+ * Across-heads RMSNorm + optional interleaved 3D RoPE, in place on a bf16 [S, heads*128] slab
+ * (row stride ld elements):  x = bf16(x * rrms * gamma), rrms = 1/sqrt(mean_row(x^2) + eps);
+ * then per pair (2i, 2i+1) of each head: (a, b) -> bf16(a cos - b sin), bf16(a sin + b cos) with
+ * cos_tab / sin_tab fp32 [S, 64] (one angle per pair; both NULL = no RoPE). gamma: fp32 [heads*128].
+ * maxnorm (optional, fp32 [heads]) receives max over tokens of each head's L2 norm of the output.
+ * Replaces DistributedRMSNorm + apply_rotary_emb_wan (vllm_omni_neuron/diffusion/models/wan2_2/
+ * wan2_2_transformer.py:879-893, diffusion/layers/rope.py:8-34) and the fused across-heads norm +
+ * RoPE epilogue of the QKV kernel (kernels/nkilib/core/qkv/qkv_cte.py:3781-3990).
+ */
+int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
+                          const float* cos_tab, const float* sin_tab, float eps, float* maxnorm,
+                          void* stream);
+
+/*
+ * V bf16, element (s, h, d) at v[s*ld + h*head_stride + d] (token-major: head_stride = 128;
+ * head-major [heads, S, 128]: ld = 128, head_stride = S*128) -> V^T [heads, 128, S_pad] bf16, keys stored inside each
+ * group of 16 in the order (0-3, 8-11, 4-7, 12-15), zero for keys >= S. S_pad % 64 == 0.
+ * The layout the attention kernel's PV product reads; no reference counterpart (the reference's
+ * attention kernels transpose internally, ring_attention_const_max_fwd.py:1180-1220).
+ */
+int wanmi_transpose_heads(const void* v, int64_t S, int64_t ld, int64_t head_stride, int heads,
+                          void* vt, int64_t S_pad, void* stream);
+
+/*
+ * out[h] = max over tokens s of ||x[h, s, :128]||_2 for a strided bf16 tensor (element (h, s, d) at
+ * x[h*head_stride + s*token_stride + d]). The key-norm input of the constant-max bound
+ * (ring_attention_const_max_fwd.py:296-360, all_reduce(max) at 1198-1205).
+ */
+int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t token_stride, int64_t S,
+                        int heads, float* out, void* stream);
+
+/* Output layouts of wanmi_attention_const_max. */
+#define WANMI_ATTN_OUT_TOKEN 0  /* bf16, element (h, s, d) at out[h*o_head + s*o_token + d] */
+#define WANMI_ATTN_OUT_DMAJOR 1 /* bf16, element (h, s, d) at out[h*o_head + d*o_d + s] ([B,N,D,S]) */
+#define WANMI_ATTN_OUT_MX 2     /* e4m3fn codes at out[h*o_head + s*o_token + d] (bytes) and e8m0
+                                   scales at out_scales[s*os_token + h*4 + d/32] */
+
+/*
+ * Non-causal constant-max attention, head_dim 128, bf16 inputs, fp32 accumulation:
+ *   o_i = sum_j exp(s q_i.k_j - c_i) v_j / max(sum_j exp(s q_i.k_j - c_i), 1e-37),
+ *   c_i = s ||q_i|| kmax[h]   (kmax[h] >= max_j ||k_j||, e.g. from wanmi_head_max_norm)
+ * q, k: element (h, s, d) at x[h*head_stride + s*token_stride + d]; vt: [heads, 128, vt_ld] from
+ * wanmi_transpose_heads (vt_ld % 64 == 0, >= Sk).
+ * Replaces ring_attention_const_max_fwd on one device (vllm_omni_neuron/kernels/nkilib/
+ * experimental/attention/ring_attention_const_max_fwd.py:959) and the flash attention behind
+ * _nki_attend / wan_cp_self_attention (diffusion/models/wan2_2/wan2_2_transformer.py:653, 806).
+ */
+int wanmi_attention_const_max(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                              const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                              const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                              int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                              void* out, int64_t o_head_stride, int64_t o_token_stride,
+                              int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                              void* stream);
+
+/*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,
  * hardware conversion; inputs must satisfy |x| < 464). Test hook for the conversion's known-answer
  * tests; it has no counterpart in the reference (which relies on torch's float8_e4m3fn cast,

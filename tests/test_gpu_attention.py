@@ -1,0 +1,161 @@
+"""GPU parity of the Q/K preparation and constant-max attention kernels.
+
+Tolerances (bf16 inputs, bf16 P, fp32 accumulation): attention outputs vs exact fp64 softmax
+attention on the same bf16 inputs: max |err| / max |ref| <= 2e-2 and cosine >= 0.999 (the stated
+bar), plus a per-element bound of 2^-6 * max|ref|. QK norm + RoPE vs the torch restatement: within
+2 bf16 ulps elementwise (multiply by reciprocal vs divide, and order of the sum of squares).
+MX output codes must equal the MX quantization of the kernel's own bf16 output, bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import mx as omx
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _check_attn(out, ref):
+    out, ref = out.double(), ref.double()
+    err = (out - ref).abs()
+    m = ref.abs().max()
+    cos = torch.nn.functional.cosine_similarity(out.flatten(), ref.flatten(), dim=0)
+    assert err.max() / m <= 2e-2 and cos >= 0.999, (float(err.max() / m), float(cos))
+    assert bool((err <= 2.0**-6 * m).all())
+
+
+@pytest.mark.parametrize("Sq,Sk,N", [(1, 1, 1), (300, 200, 2), (129, 197, 3), (64, 512, 4)])
+def test_attention_core_small(pkg, dev, Sq, Sk, N):
+    ops = pkg.attention_ops
+    q, k, v = _rand((Sq, N, 128), 1), _rand((Sk, N, 128), 2), _rand((Sk, N, 128), 3)
+    s = 128**-0.5
+    vt, _ = ops.transpose_heads(v.to(dev))
+    kmax = ops.head_max_norm(k.to(dev))
+    ref = oa.torch_attend(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), s, dtype=torch.float64)
+    tok = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_TOKEN).cpu()
+    _check_attn(tok.view(Sq, N, 128).transpose(0, 1), ref)
+    dm = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_DMAJOR).cpu()
+    _check_attn(dm.transpose(1, 2), ref)
+    torch.testing.assert_close(dm.transpose(1, 2).contiguous(), tok.view(Sq, N, 128).transpose(0, 1).contiguous(), rtol=0, atol=0)
+    mx = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_MX)
+    codes, scales = omx.mx_quantize(tok.float().numpy())
+    np.testing.assert_array_equal(mx.codes.view(torch.uint8).cpu().numpy(), codes)
+    np.testing.assert_array_equal(mx.scales.cpu().numpy(), scales)
+
+
+def test_transpose_heads_layout(pkg, dev):
+    S, N = 100, 3
+    v = _rand((S, N, 128), 5)
+    vt, S_pad = pkg.attention_ops.transpose_heads(v.to(dev))
+    assert S_pad == 128
+    order = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+    slot_key = torch.tensor([16 * (s // 16) + order[s % 16] for s in range(S_pad)])
+    ref = torch.zeros(N, 128, S_pad, dtype=torch.bfloat16)
+    vp = torch.cat([v, torch.zeros(S_pad - S, N, 128, dtype=torch.bfloat16)])
+    ref[:] = vp[slot_key].permute(1, 2, 0)
+    assert torch.equal(vt.cpu(), ref)
+
+
+def test_head_max_norm(pkg, dev):
+    k = _rand((777, 5, 128), 6, scale=2.0)
+    got = pkg.attention_ops.head_max_norm(k.to(dev)).cpu()
+    ref = k.float().norm(dim=-1).amax(dim=0)
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=0)
+
+
+def _ulps(a, b):
+    ia = a.view(torch.int16).int()
+    ib = b.view(torch.int16).int()
+    ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    return (ia - ib).abs()
+
+
+@pytest.mark.parametrize("with_rope", [True, False])
+def test_qk_rmsnorm_rope(pkg, dev, with_rope):
+    grid = (1, 30, 52)  # 1560 tokens, the single-block latent grid
+    S, N = 1560, 40
+    x = _rand((S, N * 128), 7, scale=3.0)
+    g = torch.Generator().manual_seed(8)
+    gamma = 1 + 0.02 * torch.randn(N * 128, generator=g)
+    cos, sin = orope.wan_rope(grid)
+    xd = x.to(dev).clone()
+    c64, s64 = pkg.attention_ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    kmax = pkg.attention_ops.qk_rmsnorm_rope_(
+        xd, gamma.to(dev), cos=c64 if with_rope else None, sin=s64 if with_rope else None, eps=1e-6, want_max=True
+    )
+    ref = orope.rms_norm_across_heads(x, gamma, 1e-6).view(1, S, N, 128)
+    if with_rope:
+        ref = orope.apply_rotary_emb_wan(ref, cos[None, :, None, :], sin[None, :, None, :])
+    ref = ref.view(S, N * 128)
+    got = xd.cpu()
+    u = _ulps(got, ref)
+    assert float((u > 0).float().mean()) < 0.02
+    if not with_rope:
+        assert int(u.max()) <= 2
+    else:
+        # a*cos - b*sin can cancel; bound by one bf16 ulp of the rotation-invariant pair magnitude
+        pair = ref.float().view(S, -1, 2).norm(dim=-1, keepdim=True).expand(-1, -1, 2).reshape(S, -1)
+        assert bool(((got.float() - ref.float()).abs() <= 2.0**-7 * pair + 1e-30).all())
+    torch.testing.assert_close(kmax.cpu(), xd.cpu().float().view(S, N, 128).norm(dim=-1).amax(dim=0), rtol=1e-5, atol=0)
+
+
+def test_const_max_shift_invariance_and_underflow(pkg, dev):
+    ops = pkg.attention_ops
+    q, k, v = _rand((256, 2, 128), 11), _rand((300, 2, 128), 12), _rand((300, 2, 128), 13)
+    vt, _ = ops.transpose_heads(v.to(dev))
+    kmax = ops.head_max_norm(k.to(dev))
+    s = 128**-0.5
+    a = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s).cpu().double()
+    b = ops.attention_core(q.to(dev), k.to(dev), vt, kmax * 1.5, s).cpu().double()
+    assert (a - b).abs().max() <= 2.0**-6 * a.abs().max()
+    # a bound so loose that every probability underflows: the 1e-37 floor returns zeros
+    z = ops.attention_core(q.to(dev), k.to(dev), vt, torch.full_like(kmax, 1e30), s).cpu()
+    assert bool((z == 0).all())
+
+
+def test_self_attention_full_length_rows(pkg, dev):
+    """Full self-attention sequence (21x30x52 = 32760 tokens, 40 heads, normalized + RoPE'd q/k);
+    96 query rows spread over heads and positions checked against exact fp64 attention."""
+    ops = pkg.attention_ops
+    S, N = 32760, 40
+    gdev = torch.Generator(device=dev).manual_seed(21)
+    qkv = torch.randn(S, 3 * N * 128, generator=gdev, device=dev).to(torch.bfloat16)
+    gamma = torch.ones(N * 128, device=dev)
+    cos, sin = orope.wan_rope((21, 30, 52))
+    c64, s64 = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    ops.qk_rmsnorm_rope_(qkv[:, : N * 128], gamma, cos=c64, sin=s64)
+    kmax = ops.qk_rmsnorm_rope_(qkv[:, N * 128 : 2 * N * 128], gamma, cos=c64, sin=s64, want_max=True)
+    q = qkv[:, : N * 128].view(S, N, 128)
+    k = qkv[:, N * 128 : 2 * N * 128].view(S, N, 128)
+    v = qkv[:, 2 * N * 128 :].view(S, N, 128)
+    vt, _ = ops.transpose_heads(v)
+    out = ops.attention_core(q, k, vt, kmax, 128**-0.5)
+    rows = torch.tensor([0, 1, 127, 128, 5000, 16383, 32639, 32640, 32759] + list(range(9000, 9087, 1)))[:96]
+    for h in (0, 17, 39):
+        ref = oa.torch_attend(q[rows, h].cpu(), k[:, h].cpu(), v[:, h].cpu(), 128**-0.5, dtype=torch.float64)
+        _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
+
+
+def test_dropins_match_reference_layouts(pkg, dev):
+    ops = pkg.attention_ops
+    B, N, S, D = 1, 4, 200, 128
+    q, k, v = _rand((B, S, N, D), 31), _rand((B, S, N, D), 32), _rand((B, S, N, D), 33)
+    s = D**-0.5
+    ref = oa.torch_attend(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), s, dtype=torch.float64)  # [B,N,S,D]
+    o1 = ops.wan_cp_self_attention(q.to(dev), k.to(dev), v.to(dev), s, 1, None, None).cpu()  # [B,N,D,S]
+    _check_attn(o1.transpose(2, 3), ref)
+    o2 = ops._nki_attend(q.transpose(1, 2).to(dev), k.transpose(1, 2).to(dev), v.transpose(1, 2).to(dev), s).cpu()
+    _check_attn(o2.transpose(2, 3), ref)
+    o3 = ops.ring_attention_const_max_fwd(q.to(dev), k.to(dev), v.to(dev), softmax_scale=s).cpu()  # [B,N,S,D]
+    _check_attn(o3, ref)
+    with pytest.raises(NotImplementedError):
+        ops.wan_cp_self_attention(q.to(dev), k.to(dev), v.to(dev), s, 2, None, None)

@@ -13,3 +13,11 @@ from . import _lib  # noqa: F401
 from .adaln_kernels import adaln_modulate  # noqa: F401
 from .common_types import MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401
 from .row_mx_kernels import MXWeight, mxfp8_linear, quantize_weight_mx, row_mx_mlp  # noqa: F401
+from . import attention_ops  # noqa: F401
+from .attention_ops import (  # noqa: F401
+    _nki_attend,
+    ring_attention_const_max_fwd,
+    row_mx_o_proj,
+    row_mx_qkv_proj,
+    wan_cp_self_attention,
+)

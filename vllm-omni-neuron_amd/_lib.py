@@ -33,6 +33,13 @@ _SIGNATURES = {
     "wanmi_adaln_quant": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp, _vp, _vp, _vp],
     "wanmi_e4m3_encode": [_vp, _vp, _i64, _vp],
     "wanmi_mxfp8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp],
+    "wanmi_qk_rmsnorm_rope": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _f32, _vp, _vp],
+    "wanmi_transpose_heads": [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
+    "wanmi_head_max_norm": [_vp, _i64, _i64, _i64, _i32, _vp, _vp],
+    "wanmi_attention_const_max": [
+        _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
+        _vp, _i64, _i64, _i64, _vp, _i64, _vp,
+    ],
 }
 
 _LIB = None

@@ -1,0 +1,238 @@
+"""Wan attention on gfx950: QK normalization + RoPE, constant-max attention, and the projections
+around it.
+
+Drop-ins for the reference's attention-side op boundary:
+
+- :func:`wan_cp_self_attention` (vllm_omni_neuron/diffusion/models/wan2_2/wan2_2_transformer.py:
+  806-847): token-major ``[B, S, N, D]`` q/k/v -> d-major ``[B, N, D, S]``. One GPU: ``cp_size`` must
+  be 1 (the reference's ring over a context-parallel group is the multi-GPU variant).
+- :func:`_nki_attend` (wan2_2_transformer.py:653-674): ``[B, N, S, D]`` -> ``[B, N, D, S]``.
+- :func:`ring_attention_const_max_fwd` (kernels/nkilib/experimental/attention/
+  ring_attention_const_max_fwd.py:959): token-major ``[b, S, h, d]`` -> ``[b, h, S, d]``.
+- :func:`row_mx_qkv_proj` (diffusion/quantization/row_mx_kernels.py:48-111): fused projection +
+  across-heads QK RMSNorm + RoPE.
+- :func:`row_mx_o_proj` (row_mx_kernels.py:114-138): d-major attention -> ``[B, S, H]``.
+
+All attention here is the constant-max form (exact softmax by shift invariance, no running max):
+``c_i = s ||q_i|| max_j ||k_j||`` with the key norms taken over the whole key sequence on the GPU.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .adaln_kernels import adaln_quant_2d
+from .common_types import MXTensor, NormType, QKVOutputLayout
+from .row_mx_kernels import MXWeight, _with, mxfp8_linear
+
+HEAD_DIM = 128
+OUT_TOKEN, OUT_DMAJOR, OUT_MX = 0, 1, 2
+
+
+def _pad64(n: int) -> int:
+    return (n + 63) // 64 * 64
+
+
+def rope_pair_tables(cos: torch.Tensor, sin: torch.Tensor):
+    """Wan interleaved tables ``[..., S, (1,) 128]`` -> one angle per pair, fp32 ``[S, 64]``
+    (``cos[..., 0::2]``, ``sin[..., 1::2]`` exactly as ``apply_rotary_emb_wan`` reads them)."""
+    c = cos.reshape(-1, cos.shape[-1])[:, 0::2]
+    s = sin.reshape(-1, sin.shape[-1])[:, 1::2]
+    return c.to(torch.float32).contiguous(), s.to(torch.float32).contiguous()
+
+
+def qk_rmsnorm_rope_(x: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None, eps: float = 1e-6,
+                     want_max: bool = False):
+    """In place on a bf16 ``[S, heads*128]`` view (unit column stride): across-heads RMSNorm * gamma,
+    then interleaved RoPE with pair tables ``cos``/``sin`` ``[S, 64]`` when given. Returns the
+    per-head max key norm ``[heads]`` (fp32) when ``want_max``."""
+    lib = _lib.load()
+    _lib.require_gpu(x, gamma, cos, sin, what="qk_rmsnorm_rope")
+    if x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a bf16 [S, heads*128] view with unit column stride")
+    S, W = x.shape
+    heads = W // HEAD_DIM
+    gamma = gamma.reshape(W).to(torch.float32).contiguous()
+    kmax = torch.empty(heads, dtype=torch.float32, device=x.device) if want_max else None
+    st = lib.wanmi_qk_rmsnorm_rope(
+        _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), float(eps),
+        _lib.ptr(kmax), _lib.stream_of(x),
+    )
+    _lib.check(st, "wanmi_qk_rmsnorm_rope")
+    return kmax
+
+
+def transpose_heads(v: torch.Tensor):
+    """bf16 ``[S, N, 128]`` (any strides with unit d stride) -> V^T ``[N, 128, S_pad]`` in the
+    attention kernel's key order; returns ``(vt, S_pad)``."""
+    lib = _lib.load()
+    _lib.require_gpu(v, what="transpose_heads")
+    if v.dim() != 3 or v.shape[-1] != HEAD_DIM or v.stride(2) != 1:
+        raise ValueError("v must be [S, N, 128] with unit d stride")
+    S, N, _ = v.shape
+    S_pad = _pad64(max(S, 1))
+    vt = torch.empty((N, HEAD_DIM, S_pad), dtype=torch.bfloat16, device=v.device)
+    st = lib.wanmi_transpose_heads(_lib.ptr(v), S, v.stride(0), v.stride(1), N, _lib.ptr(vt), S_pad, _lib.stream_of(v))
+    _lib.check(st, "wanmi_transpose_heads")
+    return vt, S_pad
+
+
+def head_max_norm(k: torch.Tensor) -> torch.Tensor:
+    """bf16 ``[S, N, 128]`` (unit d stride) -> fp32 ``[N]``: max over tokens of each head's norm."""
+    lib = _lib.load()
+    _lib.require_gpu(k, what="head_max_norm")
+    S, N, _ = k.shape
+    out = torch.empty(N, dtype=torch.float32, device=k.device)
+    st = lib.wanmi_head_max_norm(_lib.ptr(k), k.stride(1), k.stride(0), S, N, _lib.ptr(out), _lib.stream_of(k))
+    _lib.check(st, "wanmi_head_max_norm")
+    return out
+
+
+def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: torch.Tensor, scale: float,
+                   out_mode: int = OUT_TOKEN, out: torch.Tensor | None = None):
+    """Constant-max attention on ``[S, N, 128]`` views q (Sq) and k (Sk), V^T from
+    :func:`transpose_heads`. Returns token-major bf16 ``[Sq, N*128]``, d-major bf16
+    ``[N, 128, Sq]`` or an :class:`MXTensor` ``[Sq, N*128]``."""
+    lib = _lib.load()
+    _lib.require_gpu(q, k, vt, kmax, what="attention")
+    Sq, N, D = q.shape
+    Sk = k.shape[0]
+    if D != HEAD_DIM or k.shape[1:] != (N, D) or q.stride(2) != 1 or k.stride(2) != 1:
+        raise ValueError("q, k must be [S, N, 128] with unit d stride and matching heads")
+    dev = q.device
+    scales = None
+    if out_mode == OUT_TOKEN:
+        out = torch.empty((Sq, N * D), dtype=torch.bfloat16, device=dev) if out is None else out
+        o_hs, o_ss, o_ds = D, out.stride(0), 1
+    elif out_mode == OUT_DMAJOR:
+        out = torch.empty((N, D, Sq), dtype=torch.bfloat16, device=dev) if out is None else out
+        o_hs, o_ss, o_ds = out.stride(0), 1, out.stride(1)
+    else:
+        out = torch.empty((Sq, N * D), dtype=torch.uint8, device=dev) if out is None else out
+        scales = torch.empty((Sq, N * D // 32), dtype=torch.uint8, device=dev)
+        o_hs, o_ss, o_ds = D, out.stride(0), 1
+    st = lib.wanmi_attention_const_max(
+        _lib.ptr(q), q.stride(1), q.stride(0), _lib.ptr(k), k.stride(1), k.stride(0), _lib.ptr(vt),
+        vt.shape[-1], _lib.ptr(kmax), Sq, Sk, N, D, float(scale), out_mode, _lib.ptr(out), o_hs, o_ss, o_ds,
+        _lib.ptr(scales), 0 if scales is None else scales.stride(0), _lib.stream_of(q),
+    )
+    _lib.check(st, "wanmi_attention_const_max")
+    if out_mode == OUT_MX:
+        return MXTensor(out.view(torch.float8_e4m3fn), scales)
+    return out
+
+
+def _attend_bsnd(q, k, v, scale, out_mode):
+    """One batch element: q [Sq, N, D], k/v [Sk, N, D] (unit d stride)."""
+    vt, _ = transpose_heads(v)
+    return attention_core(q, k, vt, head_max_norm(k), scale, out_mode)
+
+
+def wan_cp_self_attention(query, key, value, scale, cp_size=1, cp_group=None, cp_replica_groups=None):
+    """Token-major ``[B, S, N, D]`` q/k/v (already normalized and rotated) -> d-major
+    ``[B, N, D, S]`` (the layout the o-projection consumes)."""
+    if cp_size != 1:
+        raise NotImplementedError("context-parallel attention spans several GPUs; this build runs on one")
+    outs = [_attend_bsnd(query[b], key[b], value[b], scale, OUT_DMAJOR) for b in range(query.shape[0])]
+    return torch.stack(outs, dim=0) if len(outs) > 1 else outs[0].unsqueeze(0)
+
+
+def _nki_attend(query, key, value, scale):
+    """Non-causal attention over ``[B, N, S, D]`` q/k/v -> d-major ``[B, N, D, S_q]``."""
+    outs = [
+        _attend_bsnd(query[b].transpose(0, 1), key[b].transpose(0, 1), value[b].transpose(0, 1), scale, OUT_DMAJOR)
+        for b in range(query.shape[0])
+    ]
+    return torch.stack(outs, dim=0) if len(outs) > 1 else outs[0].unsqueeze(0)
+
+
+def ring_attention_const_max_fwd(q, k, v, replica_groups=None, num_workers=1, softmax_scale=None,
+                                 training=False, lse_dtype=None, kv_prefetch_depth=2):
+    """Token-major ``[b, S, h, d]`` q/k/v -> ``[b, h, S, d]`` with the constant-max softmax.
+
+    One GPU holds the whole sequence, so the ring has a single member (``num_workers`` must be 1)
+    and ``kv_prefetch_depth`` has nothing to prefetch. ``training=True`` (log-sum-exp output) is not
+    part of the inference path and is rejected.
+    """
+    if num_workers != 1 or replica_groups:
+        raise NotImplementedError("a multi-member ring spans several GPUs; this build runs on one")
+    if training:
+        raise NotImplementedError("the log-sum-exp output (training=True) is not produced")
+    if q.shape[-1] != HEAD_DIM:
+        raise ValueError(f"head_dim must be 128, got {q.shape[-1]}")
+    scale = softmax_scale or 1.0 / math.sqrt(q.shape[-1])
+    outs = []
+    for b in range(q.shape[0]):
+        o = _attend_bsnd(q[b], k[b], v[b], scale, OUT_TOKEN)  # [S, h*d]
+        outs.append(o.view(q.shape[1], q.shape[2], HEAD_DIM).transpose(0, 1))
+    return torch.stack(outs, dim=0)
+
+
+def row_mx_qkv_proj(
+    packed_hidden,
+    weight: MXWeight,
+    weight_scales: torch.Tensor | None = None,
+    bias: torch.Tensor | None = None,
+    *,
+    num_heads: int,
+    head_dim: int,
+    num_kv_heads: int,
+    fused_rope: bool = False,
+    cos_cache: torch.Tensor | None = None,
+    sin_cache: torch.Tensor | None = None,
+    qk_norm_pre_rope=None,
+    qk_norm_pre_rope_q_gamma: torch.Tensor | None = None,
+    qk_norm_pre_rope_k_gamma: torch.Tensor | None = None,
+    norm_eps: float = 1e-6,
+    replica_groups=None,
+    output_layout=None,
+):
+    """Fused ``[Q | K | V]`` projection with the across-heads QK RMSNorm and RoPE applied to Q/K.
+
+    ``cos_cache``/``sin_cache`` are the reference's rotate-half caches ``[B, S, head_dim]``
+    (``cat([base, base])``, row_mx_modules.py:51-76); the rotation is applied to Wan's interleaved
+    channel pairs directly, so weights and gammas stay in their natural channel order (the reference
+    de-interleaves them offline instead, row_mx_loaders.py:26-99). Q.K is identical either way.
+    Returns bf16 ``[B, S, (nq + 2 nkv) * d]`` (BSD) or ``[N, B, S, d]`` (NBSd).
+    """
+    if head_dim != HEAD_DIM:
+        raise NotImplementedError(f"head_dim must be 128, got {head_dim}")
+    if replica_groups:
+        raise NotImplementedError("tensor-parallel replica groups span several GPUs")
+    y = mxfp8_linear(packed_hidden, _with(weight, weight_scales, bias))
+    lead = y.shape[:-1]
+    y2 = y.reshape(-1, y.shape[-1])
+    nq, nkv = num_heads, num_kv_heads
+    cos = sin = None
+    if fused_rope:
+        half = head_dim // 2
+        cos = cos_cache.reshape(-1, cos_cache.shape[-2], head_dim)[0, :, :half].to(torch.float32).contiguous()
+        sin = sin_cache.reshape(-1, sin_cache.shape[-2], head_dim)[0, :, :half].to(torch.float32).contiguous()
+        if lead.numel() // max(lead[-1], 1) != 1:
+            raise NotImplementedError("fused RoPE with batch > 1")
+    norm = qk_norm_pre_rope
+    if norm is not None and norm.q_norm == NormType.RMS_NORM_ACROSS_HEADS:
+        qk_rmsnorm_rope_(y2[:, : nq * head_dim], qk_norm_pre_rope_q_gamma, cos=cos, sin=sin, eps=norm.eps)
+    elif fused_rope:
+        raise NotImplementedError("RoPE without the across-heads norm is not on the Wan path")
+    if nkv and norm is not None and norm.k_norm == NormType.RMS_NORM_ACROSS_HEADS:
+        k_view = y2[:, nq * head_dim : (nq + nkv) * head_dim]
+        qk_rmsnorm_rope_(k_view, qk_norm_pre_rope_k_gamma, cos=cos, sin=sin, eps=norm.eps)
+    if output_layout == QKVOutputLayout.NBSd:
+        n_total = y.shape[-1] // head_dim
+        return y.reshape(*lead, n_total, head_dim).movedim(-2, 0)
+    return y
+
+
+def row_mx_o_proj(attention: torch.Tensor, weight: MXWeight, weight_scales: torch.Tensor | None = None,
+                  bias: torch.Tensor | None = None) -> torch.Tensor:
+    """d-major bf16 attention ``[B, N, D, S]`` -> ``[B, S, H]``: the activation is MX-quantized along
+    N*D (the reference's kernel quantizes it internally) and projected with the MXFP8 GEMM."""
+    B, N, D, S = attention.shape
+    x = attention.permute(0, 3, 1, 2).reshape(B * S, N * D).contiguous()
+    xq = adaln_quant_2d(x, None, None, eps=0.0, norm_type="none", quant="mx")
+    y = mxfp8_linear(xq, _with(weight, weight_scales, bias))
+    return y.reshape(B, S, -1)

@@ -1,0 +1,341 @@
+// Constant-max flash attention (non-causal) for gfx950, bf16 MFMA with fp32 accumulation.
+//
+//   o_i = sum_j exp(s q_i.k_j - c_i) v_j / max(sum_j exp(s q_i.k_j - c_i), 1e-37)
+//   c_i = s * ||q_i|| * max_j ||k_j||           (per query row; Cauchy-Schwarz bound on s q_i.k_j)
+//
+// Softmax is invariant to the subtracted constant, so no running max and no rescaling of the
+// accumulator are needed: the key loop is pure accumulation. Reference: the constant-max kernel
+// and ring driver (vllm_omni_neuron/kernels/nkilib/experimental/attention/attention_const_max.py:
+// 69-490, ring_attention_const_max_fwd.py:559-804); the exact-softmax statement is _torch_attend
+// (diffusion/models/wan2_2/wan2_2_transformer.py:640-650). Here the whole key sequence of one GPU is
+// a single "ring step", c_i is kept in fp32 (the reference rounds it to bf16; the result does not
+// depend on c), and exp runs as exp2 with log2(e) folded into the scale.
+//
+// Mapping: a workgroup owns 128 queries of one head (4 waves x 32) and walks the keys in tiles of
+// 64. Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K from LDS as the A operand,
+// its 32 queries' Q fragments resident in registers as the B operand), so every lane ends up owning
+// one query column: the row sum of P is lane-local and P^T is already laid out as the B operand of
+// O^T = V^T P^T -- no transpose of P. V^T comes pre-transposed with keys permuted inside groups of
+// 16 (wanmi_transpose_heads) to match P^T's register order. ||q_i|| is taken from the same bf16
+// Q fragments the MFMA consumes.
+#include "wanmi_common.h"
+
+namespace wanmi {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kAttnRsrcWord3 = 0x00020000;
+constexpr int BQ = 128;  // queries per workgroup
+constexpr int BKV = 64;  // keys per tile
+constexpr float kSumFloor = 1e-37f;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kAttnRsrcWord3);
+}
+
+struct AttnArgs {
+  const uint16_t* q;  // element (h, s, d) at q[h*q_hs + s*q_ss + d]
+  int64_t q_hs, q_ss;
+  const uint16_t* k;
+  int64_t k_hs, k_ss;
+  const uint16_t* vt;  // [heads, 128, vt_ld] (keys permuted within 16-groups)
+  int64_t vt_ld;
+  const float* kmax;  // [heads]
+  int64_t Sq, Sk;
+  int heads;
+  float scale;       // softmax scale s
+  float scale_log2;  // s * log2(e)
+  int out_mode;
+  void* out;
+  int64_t o_hs, o_ss, o_ds;  // token-major: (h, s, d) at o_hs*h + o_ss*s + d; d-major: + o_ds*d + s
+  uint8_t* out_scales;       // MX: [Sq, heads*4] at (s, h*4 + dtile)
+  int64_t os_ss;
+};
+
+// LDS tiles (single-buffered; 2 workgroups per CU overlap each other's loads and compute).
+//   sK: [64 keys][128 d] bf16, 16-byte chunk index XOR (key & 15)
+//   sV: [128 d][64 slots] bf16, 16-byte chunk index XOR (d & 7)
+__device__ __forceinline__ int sk_off(int key, int chunk) { return key * 256 + ((chunk ^ (key & 15)) << 4); }
+__device__ __forceinline__ int sv_off(int d, int chunk) { return d * 128 + ((chunk ^ (d & 7)) << 4); }
+
+__global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) uint8_t sK[BKV * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[128 * BKV * 2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * BQ + wave * 32;
+  const int col = lane & 31;  // this lane's query within the wave's 32
+  const int hq = lane >> 5;
+
+  // ---- Q fragments (B operand): lane holds d = 16t + 8hq .. +7 of query q0 + col, t = 0..7 ----
+  const __amdgpu_buffer_rsrc_t r_q =
+      attn_rsrc(a.q + h * a.q_hs, ((a.Sq - 1) * a.q_ss + 128) * 2);  // rows >= Sq read as zero
+  bf16x8 qf[8];
+  float qn2 = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)(((q0 + col) * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16_lo(v[j]), hi = bf16_hi(v[j]);
+      qn2 = qn2 + lo * lo;
+      qn2 = qn2 + hi * hi;
+    }
+    qf[t] = __builtin_bit_cast(bf16x8, v);
+  }
+  qn2 = qn2 + __shfl_xor(qn2, 32, 64);
+  // c_i in log2 units: s * ||q_i|| * max||k|| * log2(e)
+  const float c2 = a.scale_log2 * sqrtf(qn2) * a.kmax[h];
+
+  const __amdgpu_buffer_rsrc_t r_k = attn_rsrc(a.k + h * a.k_hs, ((a.Sk - 1) * a.k_ss + 128) * 2);
+  const __amdgpu_buffer_rsrc_t r_v = attn_rsrc(a.vt + (int64_t)h * 128 * a.vt_ld, 128 * a.vt_ld * 2);
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.0f;
+  float lsum = 0.0f;
+
+  // DMA lane mapping: K rows 16 per wave (4 per 1 KiB instruction), V rows 32 per wave (8 per KiB)
+  const int k_row = lane >> 4, k_pc = lane & 15;
+  const int v_row = lane >> 3, v_pc = lane & 7;
+
+  const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int64_t kbase = (int64_t)kt * BKV;
+    __syncthreads();  // every wave is done reading the previous tile
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = wave * 16 + i * 4 + k_row;
+      const int c = k_pc ^ (key & 15);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r_k, (__attribute__((address_space(3))) void*)(sK + (wave * 16 + i * 4) * 256), 16,
+          (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = wave * 32 + i * 8 + v_row;
+      const int c = v_pc ^ (d & 7);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r_v, (__attribute__((address_space(3))) void*)(sV + (wave * 32 + i * 8) * 128), 16,
+          (uint32_t)((d * a.vt_ld + kbase + c * 8) * 2), 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // ---- S^T = K Q^T for two 32-key sub-tiles ----
+    f32x16 s[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
+      const int key = i * 32 + col;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK + sk_off(key, 2 * t + hq));
+        s[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[i], 0, 0, 0);
+      }
+    }
+
+    // ---- P = exp2(S * s log2e - c2); lane-local row sums; pack P^T as bf16 B operands ----
+    const bool tail = kbase + BKV > a.Sk;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i][r], a.scale_log2, -c2));
+        if (tail) {
+          const int64_t key = kbase + i * 32 + (r >> 2) * 8 + hq * 4 + (r & 3);
+          x = key < a.Sk ? x : 0.0f;
+        }
+        p[r] = x;
+        lsum = lsum + x;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(p[8 * u + 2 * j], p[8 * u + 2 * j + 1]);
+        pf[i][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+      }
+    }
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = dt * 32 + col;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int g = i * 2 + u;  // 16-key group within the tile
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sV + sv_off(d, 2 * g + hq));
+          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[i][u], acc_o[dt], 0, 0, 0);
+        }
+    }
+  }
+
+  // ---- normalize and store ----
+  lsum = lsum + __shfl_xor(lsum, 32, 64);
+  const float inv = 1.0f / fmaxf(lsum, kSumFloor);
+  const int64_t qi = q0 + col;
+  const bool qok = qi < a.Sq;
+  if (a.out_mode == WANMI_ATTN_OUT_TOKEN) {
+    uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi * a.o_ss;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = dt * 32 + gi * 8 + hq * 4;
+        const float v0 = acc_o[dt][gi * 4] * inv, v1 = acc_o[dt][gi * 4 + 1] * inv;
+        const float v2 = acc_o[dt][gi * 4 + 2] * inv, v3 = acc_o[dt][gi * 4 + 3] * inv;
+        if (qok) *reinterpret_cast<uint2*>(out + d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+      }
+  } else if (a.out_mode == WANMI_ATTN_OUT_DMAJOR) {
+    uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + (r >> 2) * 8 + hq * 4 + (r & 3);
+        if (qok) out[d * a.o_ds] = (uint16_t)(pack_bf16x2(acc_o[dt][r] * inv, 0.0f) & 0xFFFFu);
+      }
+  } else {  // MX codes, token-major; a 32-wide block of d is one d tile, split between lane and lane^32
+    uint8_t* out = reinterpret_cast<uint8_t*>(a.out) + h * a.o_hs + qi * a.o_ss;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      float y[16];
+      int e = 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        y[r] = round_bf16(acc_o[dt][r] * inv);
+        e = max(e, exp_field(y[r]));
+      }
+      e = max(e, __shfl_xor(e, 32, 64));
+      const int sx = max(e - 7, 0);
+      const float f = mx_inv_scale(sx);
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = dt * 32 + gi * 8 + hq * 4;
+        const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+        if (qok) *reinterpret_cast<uint32_t*>(out + d) = c4;
+      }
+      if (qok && hq == 0) a.out_scales[qi * a.os_ss + h * 4 + dt] = (uint8_t)sx;
+    }
+  }
+}
+
+// max over tokens of the per-head L2 norm of a [S, heads, 128] (strided) bf16 tensor
+__global__ __launch_bounds__(256) void head_max_norm_kernel(const uint16_t* x, int64_t hs, int64_t ss, int64_t S,
+                                                            int heads, float* out) {
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float mx = 0.0f;
+  for (int64_t s = (int64_t)blockIdx.x * 16 + wave * 4 + (lane >> 4); s < S; s += (int64_t)gridDim.x * 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(x + h * hs + s * ss + (lane & 15) * 8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float n2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16_lo(w[j]), hi = bf16_hi(w[j]);
+      n2 += lo * lo + hi * hi;
+    }
+    n2 += __shfl_xor(n2, 1, 64);
+    n2 += __shfl_xor(n2, 2, 64);
+    n2 += __shfl_xor(n2, 4, 64);
+    n2 += __shfl_xor(n2, 8, 64);
+    mx = fmaxf(mx, sqrtf(n2));
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(out) + h, __float_as_uint(mx));
+}
+
+__global__ void attn_zero_kernel(float* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+}  // namespace wanmi
+
+extern "C" int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t token_stride, int64_t S,
+                                   int heads, float* out, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(S >= 0 && heads > 0 && heads <= 65535, WANMI_ERR_ARG, "wanmi_head_max_norm: bad S/heads");
+  WANMI_REQUIRE(out, WANMI_ERR_ARG, "wanmi_head_max_norm: out must not be null");
+  WANMI_REQUIRE(head_stride % 8 == 0 && token_stride % 8 == 0, WANMI_ERR_ARG,
+                "wanmi_head_max_norm: strides must be multiples of 8 elements");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_zero_kernel, dim3((heads + 255) / 256), dim3(256), 0, s, out, heads);
+  int st = check_launch("wanmi_head_max_norm(zero)");
+  if (st || S == 0) return st;
+  WANMI_REQUIRE(x && ((uintptr_t)x % 16) == 0, WANMI_ERR_ARG, "wanmi_head_max_norm: x must be 16-byte aligned");
+  const int64_t blocks = min((S + 15) / 16, (int64_t)256);
+  hipLaunchKernelGGL(head_max_norm_kernel, dim3((unsigned)blocks, (unsigned)heads), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), head_stride, token_stride, S, heads, out);
+  return check_launch("wanmi_head_max_norm");
+}
+
+extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                         const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                         const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                         int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                         void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                         int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                         void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(head_dim == 128, WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: head_dim must be 128, got %d",
+                head_dim);
+  WANMI_REQUIRE(Sq >= 0 && Sk > 0 && heads > 0 && heads <= 65535, WANMI_ERR_ARG,
+                "wanmi_attention_const_max: bad sizes Sq=%lld Sk=%lld heads=%d", (long long)Sq, (long long)Sk, heads);
+  WANMI_REQUIRE(out_mode >= WANMI_ATTN_OUT_TOKEN && out_mode <= WANMI_ATTN_OUT_MX, WANMI_ERR_ARG,
+                "wanmi_attention_const_max: unknown out_mode %d", out_mode);
+  WANMI_REQUIRE(vt_ld >= Sk && vt_ld % 64 == 0, WANMI_ERR_ARG,
+                "wanmi_attention_const_max: vt_ld=%lld must be >= Sk and a multiple of 64", (long long)vt_ld);
+  WANMI_REQUIRE(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && q_head_stride % 8 == 0 && k_head_stride % 8 == 0,
+                WANMI_ERR_ARG, "wanmi_attention_const_max: q/k strides must be multiples of 8 elements");
+  WANMI_REQUIRE(!(scale <= 0.0f), WANMI_ERR_ARG, "wanmi_attention_const_max: scale must be > 0");
+  if (Sq == 0) return WANMI_OK;
+  WANMI_REQUIRE(q && k && vt && kmax && out, WANMI_ERR_ARG, "wanmi_attention_const_max: null pointer");
+  WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_MX || out_scales, WANMI_ERR_ARG,
+                "wanmi_attention_const_max: MX output needs out_scales");
+  WANMI_REQUIRE(((Sq - 1) * q_token_stride + 128) * 2 < (1LL << 31) && ((Sk - 1) * k_token_stride + 128) * 2 < (1LL << 31) &&
+                    128 * vt_ld * 2 < (1LL << 31),
+                WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: per-head extent exceeds 2 GiB");
+  WANMI_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)vt % 16) == 0,
+                WANMI_ERR_ARG, "wanmi_attention_const_max: q/k/vt must be 16-byte aligned");
+  AttnArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_hs = q_head_stride;
+  a.q_ss = q_token_stride;
+  a.k = static_cast<const uint16_t*>(k);
+  a.k_hs = k_head_stride;
+  a.k_ss = k_token_stride;
+  a.vt = static_cast<const uint16_t*>(vt);
+  a.vt_ld = vt_ld;
+  a.kmax = kmax;
+  a.Sq = Sq;
+  a.Sk = Sk;
+  a.heads = heads;
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out_mode = out_mode;
+  a.out = out;
+  a.o_hs = o_head_stride;
+  a.o_ss = o_token_stride;
+  a.o_ds = o_d_stride;
+  a.out_scales = out_scales;
+  a.os_ss = os_token_stride;
+  const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
+  hipLaunchKernelGGL(attention_const_max_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("wanmi_attention_const_max");
+}

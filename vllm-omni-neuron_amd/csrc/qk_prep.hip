@@ -1,0 +1,261 @@
+// Q/K preparation for the Wan self/cross attention on gfx950.
+//
+// wanmi_qk_rmsnorm_rope: in place on a [S, heads*128] bf16 slab (row stride ld), per token:
+//   x_hat = bf16(x * rrms * gamma),  rrms = 1 / sqrt(sum(x^2) / (heads*128) + eps)     (across heads)
+//   then, if cos/sin are given, the interleaved RoPE of every (2i, 2i+1) pair in fp32:
+//   (a, b) -> bf16(a*cos - b*sin), bf16(a*sin + b*cos)
+// and optionally the per-head maximum over tokens of ||x_out|| (the const-max bound's key norm).
+// Reference: DistributedRMSNorm.forward (vllm_omni_neuron/diffusion/models/wan2_2/
+// wan2_2_transformer.py:879-893) and apply_rotary_emb_wan (diffusion/layers/rope.py:8-34); the
+// fused across-heads variant of the QKV kernel is qkv_cte.py:3781-3990. The key norm follows the
+// bound assembly of ring_attention_const_max_fwd.py:296-360, 559-642.
+//
+// wanmi_transpose_heads: V (element (s, h, d) at v[s*ld + h*head_stride + d]) -> V^T
+// [heads, 128, S_pad] with the key
+// order inside every group of 16 stored as (0-3, 8-11, 4-7, 12-15), zero for keys >= S. That is
+// the order in which the attention kernel's P^T registers hand keys to the PV MFMA, so each lane
+// reads its 8 keys with a single 16-byte LDS load.
+#include "wanmi_common.h"
+
+namespace wanmi {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+struct QKNormArgs {
+  uint16_t* x;
+  int64_t S, ld;
+  int heads, nch, tokens_per_wave;
+  const float* gamma;
+  const float* cos;  // [S, 64]
+  const float* sin;  // [S, 64]
+  float eps;
+  float* maxnorm;  // [heads] or null (must be zeroed first)
+};
+
+template <int NCH>
+__global__ __launch_bounds__(256, 2) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = a.heads * 128;
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * a.tokens_per_wave;
+  const __amdgpu_buffer_rsrc_t r_g = make_rsrc(a.gamma, 4 * (int64_t)W);
+  float kmx[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) kmx[c] = 0.0f;
+
+  for (int it = 0; it < a.tokens_per_wave; ++it) {
+    const int64_t t = t0 + it;
+    if (t >= a.S) break;  // wave-uniform
+    const __amdgpu_buffer_rsrc_t r_x = make_rsrc(a.x + t * a.ld, 2 * (int64_t)W);
+    uint32_t xp[NCH][4];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c < a.nch) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_x, lane * 16, c * 1024, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[c][j] = v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[c][j] = 0u;
+      }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = bf16_lo(xp[c][j]), v1 = bf16_hi(xp[c][j]);
+        const float q0 = v0 * v0, q1 = v1 * v1;
+        ss = ss + q0;
+        ss = ss + q1;
+      }
+    ss = wave_sum_f32(ss);
+    const float rs = (float)(1.0 / sqrt((double)(ss / (float)W) + (double)a.eps));
+
+    float cs[4], sn[4];
+    if (a.cos) {
+      const __amdgpu_buffer_rsrc_t r_c = make_rsrc(a.cos + t * 64, 256);
+      const __amdgpu_buffer_rsrc_t r_s = make_rsrc(a.sin + t * 64, 256);
+      const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(r_c, (lane & 15) * 16, 0, 0);
+      const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(r_s, (lane & 15) * 16, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cs[j] = __uint_as_float(cv[j]);
+        sn[j] = __uint_as_float(sv[j]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c < a.nch) {
+        const u32x4 g0 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32, c * 2048, 0);
+        const u32x4 g1 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32 + 16, c * 2048, 0);
+        const float gv[8] = {__uint_as_float(g0[0]), __uint_as_float(g0[1]), __uint_as_float(g0[2]),
+                             __uint_as_float(g0[3]), __uint_as_float(g1[0]), __uint_as_float(g1[1]),
+                             __uint_as_float(g1[2]), __uint_as_float(g1[3])};
+        u32x4 ov;
+        float n2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // normalized + gamma, rounded to bf16 (the reference rounds after the norm)
+          float a0 = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
+          float b0 = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
+          if (a.cos) {
+            const float ac = a0 * cs[j], bs = b0 * sn[j], as = a0 * sn[j], bc = b0 * cs[j];
+            const float r0 = ac - bs, r1 = as + bc;
+            a0 = r0;
+            b0 = r1;
+          }
+          ov[j] = pack_bf16x2(a0, b0);
+          const float fa = bf16_lo(ov[j]), fb = bf16_hi(ov[j]);
+          n2 = n2 + fa * fa;
+          n2 = n2 + fb * fb;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
+        if (a.maxnorm) {
+          // one head = 16 consecutive lanes of a chunk
+          n2 = n2 + __shfl_xor(n2, 1, 64);
+          n2 = n2 + __shfl_xor(n2, 2, 64);
+          n2 = n2 + __shfl_xor(n2, 4, 64);
+          n2 = n2 + __shfl_xor(n2, 8, 64);
+          kmx[c] = fmaxf(kmx[c], sqrtf(n2));
+        }
+      }
+    }
+  }
+  if (a.maxnorm && (lane & 15) == 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (c < a.nch)  // non-negative floats order like their bit patterns
+        atomicMax(reinterpret_cast<unsigned int*>(a.maxnorm) + c * 4 + (lane >> 4), __float_as_uint(kmx[c]));
+  }
+}
+
+__global__ void zero_f32_kernel(float* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+struct TransposeArgs {
+  const uint16_t* v;  // element (s, h, d) at v[s*ld + h*hs + d]
+  int64_t S, ld, hs;
+  int heads;
+  uint16_t* vt;
+  int64_t S_pad;
+};
+
+// Block: one head, 64 keys. LDS tile [64 keys][128 d] padded to 130 bf16 per row so the column
+// reads of the transpose hit distinct banks.
+__global__ __launch_bounds__(256) void transpose_heads_kernel(TransposeArgs a) {
+  __shared__ uint16_t tile[64][130];
+  const int h = blockIdx.y;
+  const int64_t s0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;  // 64 keys x 16 chunks of 8 d
+    const int key = idx >> 4, ch = idx & 15;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (s0 + key < a.S) v = *reinterpret_cast<const uint4*>(a.v + (s0 + key) * a.ld + h * a.hs + ch * 8);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(&tile[key][ch * 8]);
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+  }
+  __syncthreads();
+  // storage slot s of a 16-key group holds key kOrder[s]
+  const int kOrder[16] = {0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;  // 128 d x 8 chunks of 8 slots
+    const int d = idx >> 3, ch = idx & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s_lo = ch * 8 + 2 * j, s_hi = s_lo + 1;
+      const int k_lo = (s_lo & ~15) + kOrder[s_lo & 15];
+      const int k_hi = (s_hi & ~15) + kOrder[s_hi & 15];
+      w[j] = (uint32_t)tile[k_lo][d] | ((uint32_t)tile[k_hi][d] << 16);
+    }
+    if (s0 + ch * 8 < a.S_pad)
+      *reinterpret_cast<uint4*>(a.vt + ((int64_t)h * 128 + d) * a.S_pad + s0 + ch * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+}  // namespace wanmi
+
+extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
+                                     const float* cos_tab, const float* sin_tab, float eps,
+                                     float* maxnorm, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(S >= 0 && heads > 0 && heads % 4 == 0 && heads <= 128, WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope: need S >= 0 and heads a positive multiple of 4 (<= 128), got S=%lld heads=%d",
+                (long long)S, heads);
+  WANMI_REQUIRE(ld >= heads * 128 && ld % 8 == 0, WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope: bad ld=%lld", (long long)ld);
+  WANMI_REQUIRE((cos_tab == nullptr) == (sin_tab == nullptr), WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope: cos and sin must both be given or both be null");
+  WANMI_REQUIRE(!(eps < 0.0f), WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope: eps must be >= 0");
+  hipStream_t s = (hipStream_t)stream;
+  if (maxnorm) {
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((heads + 255) / 256), dim3(256), 0, s, maxnorm, heads);
+    int st = check_launch("wanmi_qk_rmsnorm_rope(zero)");
+    if (st) return st;
+  }
+  if (S == 0) return WANMI_OK;
+  WANMI_REQUIRE(x && gamma, WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope: x and gamma must not be null");
+  WANMI_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)gamma % 16) == 0 &&
+                    (!cos_tab || (((uintptr_t)cos_tab % 16) == 0 && ((uintptr_t)sin_tab % 16) == 0)),
+                WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope: tensors must be 16-byte aligned");
+  QKNormArgs a;
+  a.x = static_cast<uint16_t*>(x);
+  a.S = S;
+  a.ld = ld;
+  a.heads = heads;
+  a.nch = heads / 4;
+  a.tokens_per_wave = 8;
+  a.gamma = gamma;
+  a.cos = cos_tab;
+  a.sin = sin_tab;
+  a.eps = eps;
+  a.maxnorm = maxnorm;
+  const int64_t waves = (S + a.tokens_per_wave - 1) / a.tokens_per_wave;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  if (a.nch <= 4) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<4>, grid, dim3(256), 0, s, a);
+  else if (a.nch <= 10) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<10>, grid, dim3(256), 0, s, a);
+  else if (a.nch <= 16) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<16>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<32>, grid, dim3(256), 0, s, a);
+  return check_launch("wanmi_qk_rmsnorm_rope");
+}
+
+extern "C" int wanmi_transpose_heads(const void* v, int64_t S, int64_t ld, int64_t head_stride, int heads,
+                                     void* vt, int64_t S_pad, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(S >= 0 && heads > 0 && heads <= 65535, WANMI_ERR_ARG, "wanmi_transpose_heads: bad S/heads");
+  WANMI_REQUIRE(S_pad >= S && S_pad % 64 == 0, WANMI_ERR_ARG,
+                "wanmi_transpose_heads: S_pad=%lld must be >= S and a multiple of 64", (long long)S_pad);
+  WANMI_REQUIRE(ld >= 128 && ld % 8 == 0 && head_stride % 8 == 0, WANMI_ERR_ARG,
+                "wanmi_transpose_heads: bad ld=%lld / head_stride=%lld", (long long)ld, (long long)head_stride);
+  if (S_pad == 0) return WANMI_OK;
+  WANMI_REQUIRE(v && vt, WANMI_ERR_ARG, "wanmi_transpose_heads: null pointer");
+  WANMI_REQUIRE(((uintptr_t)v % 16) == 0 && ((uintptr_t)vt % 16) == 0, WANMI_ERR_ARG,
+                "wanmi_transpose_heads: tensors must be 16-byte aligned");
+  TransposeArgs a;
+  a.v = static_cast<const uint16_t*>(v);
+  a.S = S;
+  a.ld = ld;
+  a.hs = head_stride;
+  a.heads = heads;
+  a.vt = static_cast<uint16_t*>(vt);
+  a.S_pad = S_pad;
+  hipLaunchKernelGGL(transpose_heads_kernel, dim3((unsigned)(S_pad / 64), (unsigned)heads), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return check_launch("wanmi_transpose_heads");
+}
