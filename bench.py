@@ -1,0 +1,239 @@
+"""Benchmark: one Wan2.2-A14B DiT forward (40 blocks) at 32760 video tokens on one MI355X.
+
+Workload: 40 Wan2.2-A14B blocks (dim 5120, 40 heads x 128, FFN 13824), S = 32760 tokens
+(21x30x52 latent grid, 480x832x81 frames), 512 text tokens, MXFP8 projections and bf16 constant-max
+attention, one CFG branch, cross-attention K/V cached (projected once before timing, as the
+reference does per generation). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
+seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic data.
+
+Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). Per-kernel times
+come from HIP events recorded around every launch inside the timed steps; the roofline entry is the
+dominant kernel (self-attention). The CPU baseline is the reference's BF16 eager block (restated
+in the oracle) timed on this host's cores at the 1560-token block shape, extrapolated to the step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import __graft_entry__  # noqa: E402
+
+DIM, HEADS, HEAD_DIM, FFN, TXT = 5120, 40, 128, 13824, 512
+PEAK_BF16_TFLOPS, PEAK_FP8_TFLOPS, PEAK_HBM_GBS = 2500.0, 5000.0, 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--grid", type=str, default="21,30,52", help="latent patch grid F,H,W")
+    p.add_argument("--blocks", type=int, default=40)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+class KernelTimer:
+    """Records HIP events (on the launching stream) around each kernel call of the timed steps."""
+
+    def __init__(self):
+        self.active = False
+        self.events = {}
+
+    def __call__(self, name, fn):
+        if not self.active:
+            return fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = fn()
+        e.record()
+        self.events.setdefault(name, []).append((s, e))
+        return r
+
+    def summary(self):
+        return {k: [s.elapsed_time(e) for s, e in v] for k, v in self.events.items()}
+
+
+def gemm_flops(S):
+    return 2 * S * (DIM * 3 * DIM + DIM * DIM + DIM * DIM + DIM * DIM + 2 * DIM * FFN)
+
+
+def cpu_baseline(S_full, blocks):
+    """Reference BF16 eager block on the host CPU at the 1560-token shape; extrapolated to the
+    step: projections/FFN/cross-attention linearly in S, self-attention quadratically."""
+    from oracle import block as oblock
+    from oracle import rope as orope
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    grid = (1, 30, 52)
+    S = 1560
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    raw = {
+        "scale_shift_table": torch.randn(6, DIM, generator=g) * 0.02,
+        "qkv_w": (torch.randn(DIM, 3 * DIM, generator=g) * 0.02).to(bf), "qkv_b": torch.randn(3 * DIM, generator=g) * 0.02,
+        "norm_q": 1 + torch.randn(DIM, generator=g) * 0.02, "norm_k": 1 + torch.randn(DIM, generator=g) * 0.02,
+        "o_w": (torch.randn(DIM, DIM, generator=g) * 0.02).to(bf), "o_b": torch.randn(DIM, generator=g) * 0.02,
+        "norm2_weight": torch.randn(DIM, generator=g) * 0.02, "norm2_bias": torch.randn(DIM, generator=g) * 0.02,
+        "q2_w": (torch.randn(DIM, DIM, generator=g) * 0.02).to(bf), "q2_b": torch.randn(DIM, generator=g) * 0.02,
+        "k2_w": (torch.randn(DIM, DIM, generator=g) * 0.02).to(bf), "k2_b": torch.randn(DIM, generator=g) * 0.02,
+        "v2_w": (torch.randn(DIM, DIM, generator=g) * 0.02).to(bf), "v2_b": torch.randn(DIM, generator=g) * 0.02,
+        "norm_q2": 1 + torch.randn(DIM, generator=g) * 0.02, "norm_k2": 1 + torch.randn(DIM, generator=g) * 0.02,
+        "o2_w": (torch.randn(DIM, DIM, generator=g) * 0.02).to(bf), "o2_b": torch.randn(DIM, generator=g) * 0.02,
+        "up_w": (torch.randn(DIM, FFN, generator=g) * 0.02).to(bf), "up_b": torch.randn(FFN, generator=g) * 0.02,
+        "down_w": (torch.randn(FFN, DIM, generator=g) * 0.02).to(bf), "down_b": torch.randn(DIM, generator=g) * 0.02,
+    }
+    h = torch.randn(S, DIM, generator=g).to(bf)
+    temb = torch.randn(6, DIM, generator=g)
+    ctx = torch.randn(TXT, DIM, generator=g).to(bf)
+
+    def run_block():
+        return oblock.bf16_eager_block(raw, h, temb, ctx, grid)
+
+    q = torch.randn(1, HEADS, S, HEAD_DIM, generator=g).to(bf)
+
+    def run_self_attn():  # the block's self-attention core alone (_torch_attend on [B, N, S, D])
+        sc = torch.matmul(q.float() * HEAD_DIM**-0.5, q.float().transpose(-2, -1))
+        return torch.matmul(torch.softmax(sc, dim=-1), q.float()).to(bf)
+
+    def med(fn, n=3):
+        fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    t_block = med(run_block)
+    t_attn = min(med(run_self_attn), t_block)
+    r = S_full / S
+    step_ms = blocks * ((t_block - t_attn) * r + t_attn * r * r) * 1000.0
+    return {
+        "value": round(step_ms, 1),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference BF16 eager block (oracle restatement: _eager_adaln, torch.matmul, "
+                   f"DistributedRMSNorm, RoPE, _torch_attend, GELU-tanh FFN) at S=1560 (1x30x52), 512 text "
+                   f"tokens, median of 3 after 1 warm-up: {t_block * 1000:.0f} ms/block, of which self-attention "
+                   f"{t_attn * 1000:.0f} ms; extrapolated to {blocks} blocks at S={S_full} (self-attention x{r * r:.0f}, "
+                   f"the rest x{r:.1f})"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} requested, but this build runs on one GPU only "
+              "(no collectives or sharding); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    pkg = __graft_entry__.load_package()
+    from oracle import rope as orope  # RoPE tables are host-side constants (not timed)
+
+    dev = torch.device("cuda:0")
+    grid = tuple(int(x) for x in args.grid.split(","))
+    S = grid[0] * grid[1] * grid[2]
+    blk, ops = pkg.block, pkg.attention_ops
+
+    gen = torch.Generator(device=dev).manual_seed(2024)
+    blocks = [blk.random_block_weights(dev, gen, qk_gamma_mean=1.0, keep_raw=False)[0] for _ in range(args.blocks)]
+    h0 = torch.randn(S, DIM, device=dev, generator=gen).to(torch.bfloat16)
+    temb = torch.randn(6, DIM, device=dev, generator=gen)
+    ctx = torch.randn(TXT, DIM, device=dev, generator=gen).to(torch.bfloat16)
+    cos, sin = orope.wan_rope(grid)
+    rope = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    crosses = [blk.project_cross_kv(w, ctx) for w in blocks]
+    torch.cuda.synchronize()
+
+    timer = KernelTimer()
+    for _ in range(args.warmup):
+        blk.dit_forward(blocks, h0, temb, rope, crosses)
+    torch.cuda.synchronize()
+
+    timer.active = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = blk.dit_forward(blocks, h0, temb, rope, crosses, timer=timer)
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t0) * 1000.0
+    timer.active = False
+    ms_step = total_ms / args.steps
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("non-finite DiT output")
+
+    times = timer.summary()
+    n_blk = args.steps * args.blocks
+
+    def avg(name):
+        return sum(times[name]) / len(times[name])
+
+    attn_flops = 4.0 * S * S * HEAD_DIM * HEADS
+    attn_ms = avg("self_attention")
+    attn_tflops = attn_flops / attn_ms / 1e9
+    gemm_names = [k for k in times if k.startswith("gemm_")]
+    gemm_ms = sum(sum(times[k]) for k in gemm_names) / n_blk
+    gemm_tflops = gemm_flops(S) / gemm_ms / 1e9
+    # adaLN: first launch of each block is the plain modulation (x read, MX codes + scales written);
+    # the second and third also read the residual and write the bf16 residual sum.
+    plain = 2 * S * DIM + S * DIM + S * DIM // 32 + 2 * DIM * 4
+    fused = 2 * 2 * S * DIM + 2 * S * DIM + S * DIM + S * DIM // 32 + 3 * DIM * 4
+    ad = times["adaln"]
+    ad_bytes = [plain if i % 3 == 0 else fused for i in range(len(ad))]
+    adaln_gbs = sum(ad_bytes) / sum(ad) / 1e6
+    first_adaln_us = sum(ad[0::3]) / len(ad[0::3]) * 1000.0
+    comp = {k: {"ms_per_launch": round(sum(v) / len(v), 4), "ms_per_step": round(sum(v) / args.steps, 2)}
+            for k, v in sorted(times.items())}
+
+    result = {
+        "metric": "DiT step ms @32760 tok (A14B); attn+GEMM TFLOP/s; adaLN-quant GB/s",
+        "value": round(ms_step, 2),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp8 projections (fp32 acc) + bf16 attention (fp32 acc)",
+        "data": "synthetic (seeded N(0,1) activations, random N(0,0.02) weights)",
+        "config": {
+            "workload": "Wan2.2-A14B DiT forward: 40 blocks, one CFG branch, cross-attn K/V cached",
+            "seq_len": S, "grid": list(grid), "blocks": args.blocks, "text_tokens": TXT, "dim": DIM,
+            "heads": HEADS, "head_dim": HEAD_DIM, "ffn": FFN, "parallelism": "none (1 GPU)",
+        },
+        "attn_tflops": round(attn_tflops, 1),
+        "gemm_tflops": round(gemm_tflops, 1),
+        "adaln_quant_gbs": round(adaln_gbs, 1),
+        "adaln_quant_us_32760x5120": round(first_adaln_us, 1),
+        "components": comp,
+        "roofline": {
+            "kernel": "attention_const_max_kernel (self-attention, S=32760, 40 heads x 128)",
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(S, args.blocks)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

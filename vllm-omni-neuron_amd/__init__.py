@@ -21,3 +21,4 @@ from .attention_ops import (  # noqa: F401
     row_mx_qkv_proj,
     wan_cp_self_attention,
 )
+from . import block  # noqa: F401

@@ -1,0 +1,144 @@
+"""The Wan2.2 DiT transformer block and the 40-block forward on the gfx950 kernels.
+
+Follows ``WanTransformerBlock.forward`` (vllm_omni_neuron/diffusion/models/wan2_2/
+wan2_2_transformer.py:1428-1513) with every projection in MXFP8 and attention in bf16:
+
+    e = scale_shift_table + temb                     -> shift, scale, gate, c_shift, c_scale, c_gate
+    a1 = MX(LN(h) * (1 + scale) + shift)              adaLN kernel
+    qkv = a1 @ Wqkv + b                               MXFP8 GEMM
+    q, k = RoPE(RMS_heads(q) g_q), RoPE(RMS_heads(k) g_k); V^T      prep kernels
+    o1 = MX(attention(q, k, v))                       constant-max attention, MX epilogue
+    h1, a2 = h + gate * (o1 @ Wo + b),  MX(LN_affine(h1))            GEMM + adaLN (fused residual)
+    q2 = RMS_heads(a2 @ Wq2 + b) g_q2; o2 = MX(attention(q2, K2, V2)) cross-attention (cached K2/V2)
+    h2, a3 = h1 + (o2 @ Wo2 + b),  MX(LN(h2) * (1 + c_scale) + c_shift)
+    h3 = h2 + c_gate * (MX(GELU_tanh(a3 @ Wup + b)) @ Wdown + b)     GEMM (GELU+MX) + GEMM (gated residual)
+
+The cross-attention K/V depend only on the text context, so -- as in the reference
+(``forward_and_cache_cross_attention_kv``, wan2_2_transformer.py:1675-1725) -- they are projected once
+per generation by :func:`project_cross_kv` and reused by every step. The 40-block loop is
+``WanTransformer3DModel.forward``'s (wan2_2_transformer.py:1818-1825).
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import attention_ops as ops
+from .adaln_kernels import adaln_quant_2d
+from .row_mx_kernels import MXWeight, mxfp8_linear, quantize_weight_mx
+
+DIM, HEADS, HEAD_DIM, FFN = 5120, 40, 128, 13824
+
+
+class BlockWeights(NamedTuple):
+    scale_shift_table: torch.Tensor  # fp32 [6, DIM]
+    qkv: MXWeight  # [3*DIM, DIM]
+    norm_q: torch.Tensor  # fp32 [DIM]
+    norm_k: torch.Tensor
+    o: MXWeight
+    norm2_weight: torch.Tensor  # fp32 [DIM] (affine LayerNorm of the cross-attention input)
+    norm2_bias: torch.Tensor
+    q2: MXWeight
+    k2: MXWeight
+    v2: MXWeight
+    norm_q2: torch.Tensor
+    norm_k2: torch.Tensor
+    o2: MXWeight
+    up: MXWeight  # [FFN, DIM]
+    down: MXWeight  # [DIM, FFN]
+
+
+class CrossKV(NamedTuple):
+    k: torch.Tensor  # bf16 [S_txt, HEADS, 128], normalized
+    vt: torch.Tensor  # bf16 [HEADS, 128, S_pad]
+    kmax: torch.Tensor  # fp32 [HEADS]
+
+
+def random_block_weights(device, generator=None, std: float = 0.02, dim: int = DIM, ffn: int = FFN,
+                         heads: int = HEADS, qk_gamma_mean: float = 0.0, keep_raw: bool = True):
+    """Random-init block (weights N(0, std) in bf16, quantized to MX on the GPU). Returns the GEMM
+    layout weights and (``keep_raw``) the bf16 reference-layout tensors they came from (``x @ W``)."""
+
+    def rnd(*shape):
+        return (torch.randn(*shape, device=device, generator=generator) * std).to(torch.bfloat16)
+
+    def vec(n, mean=0.0):
+        return (mean + torch.randn(n, device=device, generator=generator) * std).float()
+
+    raw = {
+        "scale_shift_table": vec(6 * dim).view(6, dim),
+        "qkv_w": rnd(dim, 3 * dim), "qkv_b": vec(3 * dim),
+        "norm_q": vec(dim, qk_gamma_mean), "norm_k": vec(dim, qk_gamma_mean),
+        "o_w": rnd(dim, dim), "o_b": vec(dim),
+        "norm2_weight": vec(dim), "norm2_bias": vec(dim),
+        "q2_w": rnd(dim, dim), "q2_b": vec(dim),
+        "k2_w": rnd(dim, dim), "k2_b": vec(dim),
+        "v2_w": rnd(dim, dim), "v2_b": vec(dim),
+        "norm_q2": vec(dim, qk_gamma_mean), "norm_k2": vec(dim, qk_gamma_mean),
+        "o2_w": rnd(dim, dim), "o2_b": vec(dim),
+        "up_w": rnd(dim, ffn), "up_b": vec(ffn),
+        "down_w": rnd(ffn, dim), "down_b": vec(dim),
+    }
+    q = lambda n: quantize_weight_mx(raw[n + "_w"], raw[n + "_b"])  # noqa: E731
+    w = BlockWeights(
+        raw["scale_shift_table"], q("qkv"), raw["norm_q"], raw["norm_k"], q("o"), raw["norm2_weight"],
+        raw["norm2_bias"], q("q2"), q("k2"), q("v2"), raw["norm_q2"], raw["norm_k2"], q("o2"), q("up"), q("down"),
+    )
+    return w, (raw if keep_raw else None)
+
+
+def project_cross_kv(w: BlockWeights, context: torch.Tensor, eps: float = 1e-6) -> CrossKV:
+    """Text context ``[S_txt, DIM]`` bf16 -> normalized K, V^T and the key-norm bound (once per
+    generation; the reference row-packs the context once and projects K/V per expert)."""
+    ctx = adaln_quant_2d(context.contiguous(), None, None, eps=0.0, norm_type="none", quant="mx")
+    k = mxfp8_linear(ctx, w.k2)
+    kmax = ops.qk_rmsnorm_rope_(k, w.norm_k2, eps=eps, want_max=True)
+    v = mxfp8_linear(ctx, w.v2)
+    heads = k.shape[1] // HEAD_DIM
+    vt, _ = ops.transpose_heads(v.view(-1, heads, HEAD_DIM))
+    return CrossKV(k.view(-1, heads, HEAD_DIM), vt, kmax)
+
+
+def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cross: CrossKV,
+                  eps: float = 1e-6, timer=None) -> torch.Tensor:
+    """One block on ``h`` bf16 ``[S, DIM]``; ``temb`` ``[6, DIM]`` (or ``[1, 6, DIM]``); ``rope`` is
+    ``(cos, sin)`` pair tables ``[S, 64]``. ``timer(name, fn)`` optionally wraps each kernel launch."""
+    run = timer or (lambda name, fn: fn())
+    S, dim = h.shape
+    heads = dim // HEAD_DIM
+    scale = HEAD_DIM**-0.5
+    e = w.scale_shift_table + temb.reshape(6, dim).float()
+    shift, sc, gate, c_shift, c_sc, c_gate = (e[i].contiguous() for i in range(6))
+    one_p_sc, one_p_csc = (1 + sc).contiguous(), (1 + c_sc).contiguous()
+    cos, sin = rope
+
+    a1 = run("adaln", lambda: adaln_quant_2d(h, one_p_sc, shift, eps=eps, norm_type="layer_norm", quant="mx"))
+    qkv = run("gemm_qkv", lambda: mxfp8_linear(a1, w.qkv))
+    run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qkv[:, :dim], w.norm_q, cos=cos, sin=sin, eps=eps))
+    kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qkv[:, dim : 2 * dim], w.norm_k, cos=cos, sin=sin, eps=eps,
+                                                      want_max=True))
+    vt, _ = run("v_transpose", lambda: ops.transpose_heads(qkv[:, 2 * dim :].view(S, heads, HEAD_DIM)))
+    q = qkv[:, :dim].view(S, heads, HEAD_DIM)
+    k = qkv[:, dim : 2 * dim].view(S, heads, HEAD_DIM)
+    o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX))
+    attn1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o))
+    h1, a2 = run("adaln", lambda: adaln_quant_2d(attn1, w.norm2_weight, w.norm2_bias, eps=eps, norm_type="layer_norm",
+                                                quant="mx", residual=h, gate=gate))
+    q2 = run("gemm_q2", lambda: mxfp8_linear(a2, w.q2))
+    run("qk_prep", lambda: ops.qk_rmsnorm_rope_(q2, w.norm_q2, eps=eps))
+    o2 = run("cross_attention", lambda: ops.attention_core(q2.view(S, heads, HEAD_DIM), cross.k, cross.vt, cross.kmax,
+                                                          scale, ops.OUT_MX))
+    attn2 = run("gemm_o2", lambda: mxfp8_linear(o2, w.o2))
+    h2, a3 = run("adaln", lambda: adaln_quant_2d(attn2, one_p_csc, c_shift, eps=eps, norm_type="layer_norm", quant="mx",
+                                                residual=h1, gate=None))
+    inter = run("gemm_up", lambda: mxfp8_linear(a3, w.up, epilogue="gelu_mx"))
+    return run("gemm_down", lambda: mxfp8_linear(inter, w.down, epilogue="gated_residual", residual=h2, gate=c_gate))
+
+
+def dit_forward(blocks, h: torch.Tensor, temb: torch.Tensor, rope, crosses, eps: float = 1e-6, timer=None):
+    """The 40-block loop of one DiT forward (one CFG branch), cross-attention K/V cached."""
+    for w, cross in zip(blocks, crosses):
+        h = block_forward(w, h, temb, rope, cross, eps, timer)
+    return h
