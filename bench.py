@@ -40,7 +40,23 @@ def parse():
     p.add_argument("--grid", type=str, default="21,30,52", help="latent patch grid F,H,W")
     p.add_argument("--blocks", type=int, default=40)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--pmc-calibration", action="store_true",
+                   help="also run one 256 MiB device copy, the known-size reference for HBM counters")
     return p.parse_args()
+
+
+def load_traffic():
+    """HBM bytes per self-attention launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (scaled by the same counters on a known-size copy); committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", "self_attention_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            key, _, val = line.partition("=")
+            if key.strip() == "self_attention_bytes_per_launch":
+                return float(val)
+    return None
 
 
 class KernelTimer:
@@ -157,6 +173,13 @@ def main():
     crosses = [blk.project_cross_kv(w, ctx) for w in blocks]
     torch.cuda.synchronize()
 
+    if args.pmc_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     timer = KernelTimer()
     for _ in range(args.warmup):
         blk.dit_forward(blocks, h0, temb, rope, crosses)
@@ -227,7 +250,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": load_traffic(),
         },
     }
     if not args.no_cpu_baseline:

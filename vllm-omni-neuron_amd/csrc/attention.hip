@@ -57,6 +57,9 @@ struct AttnArgs {
 __device__ __forceinline__ int sk_off(int key, int chunk) { return key * 256 + ((chunk ^ (key & 15)) << 4); }
 __device__ __forceinline__ int sv_off(int d, int chunk) { return d * 128 + ((chunk ^ (d & 7)) << 4); }
 
+// kShortKV: a separate instantiation for short key sequences (cross-attention over text tokens) so
+// the two uses can be specialized and profiled apart.
+template <bool kShortKV>
 __global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) uint8_t sK[BKV * 256];
@@ -336,6 +339,9 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   a.out_scales = out_scales;
   a.os_ss = os_token_stride;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
-  hipLaunchKernelGGL(attention_const_max_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+  if (Sk <= 1024)
+    hipLaunchKernelGGL(attention_const_max_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(attention_const_max_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("wanmi_attention_const_max");
 }
