@@ -14,10 +14,12 @@
 // (e4m3) vectors.
 //
 // Tiling: 256 (n) x 256 (m) x 128 (k) per workgroup of 4 waves, each wave a 128 x 128 block of
-// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand tiles are staged through LDS, double
-// buffered and filled by direct-to-LDS loads (global_load_lds_dwordx4), with a 16-byte-chunk XOR
-// swizzle (chunk ^ (row & 7)) so the MFMA operand reads of eight consecutive rows land on distinct
-// banks. Workgroup ids are remapped so each XCD (ids are
+// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand tiles are staged through LDS in two
+// stage buffers filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds, no VGPR round
+// trip), with a 16-byte-chunk XOR swizzle (chunk ^ (row & 7)) so the MFMA operand reads of eight
+// consecutive rows land on distinct banks. Each stage's loads are issued two stages ahead into the
+// buffer just consumed; operands are read per 64-deep slice into ping-pong registers so LDS reads
+// overlap the previous slice's MFMAs. Workgroup ids are remapped so each XCD (ids are
 // dealt round-robin over 8 XCDs) works on a contiguous, L2-friendly group of tiles.
 //
 // Reference semantics: the ROW_MX projection epilogues of _qkv_cte_mx_impl / _dequant_row_mx
@@ -35,6 +37,9 @@ constexpr int BK = 128;  // k bytes per stage (4 MX blocks)
 constexpr int kStageBytes = TN * BK + TM * BK + TN * 4 + TM * 4;
 constexpr int kGroupM = 8;
 constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
+constexpr int kWaitVm18 = (18 & 0xF) | (0x7 << 4) | (0xF << 8) | ((18 >> 4) << 14);  // vmcnt <= 18
+constexpr int kWaitLgkm0 = 0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14);               // lgkmcnt == 0
 
 struct GemmArgs {
   const uint8_t* a;         // [M, lda]
@@ -64,57 +69,47 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
 
 
-// MFMA operands of one 128-deep k step of a wave's 128 x 128 block: 2 k-slices of 64, each with
-// 4 weight-row and 4 token-row fragments (32 bytes per lane) and their e8m0 scale bytes.
-struct StageOperands {
-  i32x8 w[2][4];
-  i32x8 a[2][4];
-  int ws[2][4];
-  int as[2][4];
+// MFMA operands of one 64-deep k slice of a wave's 128 x 128 block: 4 weight-row and 4 token-row
+// fragments (32 bytes per lane each) and their e8m0 scale bytes.
+struct SliceOperands {
+  i32x8 w[4];
+  i32x8 a[4];
+  int ws[4];
+  int as[4];
 };
 
-__device__ __forceinline__ void read_stage(const uint8_t* base, StageOperands& op, int wn, int wm, int h, int r32) {
+// Reads slice s (0 or 1) of an LDS stage. Lane data: bytes 0-15 = k[64s + 16h, +16),
+// bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of its row.
+__device__ __forceinline__ void read_slice(const uint8_t* base, int s, SliceOperands& op, int wn, int wm, int h,
+                                           int r32) {
   const uint8_t* sw = base;
   const uint8_t* sa = base + TN * BK;
   const uint32_t* sws = reinterpret_cast<const uint32_t*>(base + TN * BK + TM * BK);
   const uint32_t* sas = sws + TN;
+  const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
+  const int sh = 8 * (2 * s + h);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t wsc = sws[wn * 128 + i * 32 + r32];
-    const uint32_t asc = sas[wm * 128 + i * 32 + r32];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      op.ws[s][i] = (int)((wsc >> (8 * (2 * s + h))) & 0xFFu);
-      op.as[s][i] = (int)((asc >> (8 * (2 * s + h))) & 0xFFu);
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    // lane data: bytes 0-15 = k[64s + 16h, +16), bytes 16-31 = k[64s + 32 + 16h, +16)
-    const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rw = wn * 128 + i * 32 + r32;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(sw + swz(rw, c0));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(sw + swz(rw, c1));
-      op.w[s][i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-      const int ra = wm * 128 + i * 32 + r32;
-      const uint4 y0 = *reinterpret_cast<const uint4*>(sa + swz(ra, c0));
-      const uint4 y1 = *reinterpret_cast<const uint4*>(sa + swz(ra, c1));
-      op.a[s][i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
-    }
+    const int rw = wn * 128 + i * 32 + r32;
+    const uint4 x0 = *reinterpret_cast<const uint4*>(sw + swz(rw, c0));
+    const uint4 x1 = *reinterpret_cast<const uint4*>(sw + swz(rw, c1));
+    op.w[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    const int ra = wm * 128 + i * 32 + r32;
+    const uint4 y0 = *reinterpret_cast<const uint4*>(sa + swz(ra, c0));
+    const uint4 y1 = *reinterpret_cast<const uint4*>(sa + swz(ra, c1));
+    op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
+    op.ws[i] = (int)((sws[rw] >> sh) & 0xFFu);
+    op.as[i] = (int)((sas[ra] >> sh) & 0xFFu);
   }
 }
 
-__device__ __forceinline__ void mfma_stage(const StageOperands& op, f32x16 (&acc)[4][4]) {
+__device__ __forceinline__ void mfma_slice(const SliceOperands& op, f32x16 (&acc)[4][4]) {
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[s][i], op.a[s][j], acc[i][j], 0, 0, 0,
-                                                                     op.ws[s][i], 0, op.as[s][j]);
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
+                                                                   op.as[j]);
 }
 
 // One 32 x 32 accumulator tile: lane holds token m and n = ntile + 8*gi + 4*h + q (gi, q in 0..3).
@@ -204,9 +199,15 @@ __device__ __forceinline__ void epilogue_all(const GemmArgs& g, const f32x16 (&a
   }
 }
 
+// kEvenStages: the pipelined, branch-free loop below (K a multiple of 256); otherwise a simple
+// double-buffered loop that issues the next stage's loads after all reads of the current one.
+template <bool kEvenStages>
 __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];
+  // Two separate LDS objects: the compiler can then prove that the stage being read never aliases
+  // the stage being filled by in-flight direct-to-LDS loads, and waits only on the latter's own.
+  __shared__ __attribute__((aligned(16))) uint8_t smem0[kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem1[kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -278,22 +279,61 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
   const int h = lane >> 5;
   const int r32 = lane & 31;
 
-  WANMI_GEMM_ISSUE(0, smem);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // Per k step: read every MFMA operand of the current stage from LDS, then issue the direct-to-LDS
-  // loads of the next stage into the other buffer (last read before the previous barrier), then run
-  // the 32 MFMAs while those loads are in flight.
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    StageOperands op;
-    read_stage(smem + cur * kStageBytes, op, wn, wm, h, r32);
-    if (kt + 1 < KT) WANMI_GEMM_ISSUE(kt + 1, smem + (cur ^ 1) * kStageBytes);
-    mfma_stage(op, acc);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
-    __syncthreads();                 // ... and everyone's; the next stage is readable
+  if constexpr (!kEvenStages) {
+    // stage kt in smem0 / smem1 alternately; the next stage's loads go into the other buffer
+    // (read by nobody since the previous barrier) before this stage's MFMAs
+    WANMI_GEMM_ISSUE(0, smem0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      uint8_t* cur = (kt & 1) ? smem1 : smem0;
+      uint8_t* nxt = (kt & 1) ? smem0 : smem1;
+      if (kt + 1 < KT) WANMI_GEMM_ISSUE(kt + 1, nxt);
+      SliceOperands op;
+      read_slice(cur, 0, op, wn, wm, h, r32);
+      mfma_slice(op, acc);
+      read_slice(cur, 1, op, wn, wm, h, r32);
+      mfma_slice(op, acc);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  } else {
+    // Pipeline (KT even, branch-free): stage kt lives in smem0 for even kt, smem1 for odd kt. The
+    // loads of stage kt+2 go into the buffer stage kt was just read from (after a barrier confirms
+    // every wave has read it), so each stage's loads have two stages of MFMA work to land; past the
+    // end the stage index is clamped, re-loading the last stage into a buffer nobody reads again.
+    // Within a stage the two 64-deep slices are read into ping-pong registers, each slice's LDS
+    // reads overlapping the previous slice's MFMAs.
+    WANMI_GEMM_ISSUE(0, smem0);
+    WANMI_GEMM_ISSUE(1, smem1);
+    __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage 0 landed (stage 1's 18 loads may be in flight)
+    __syncthreads();
+    SliceOperands opA, opB;
+    read_slice(smem0, 0, opA, wn, wm, h, r32);
+    for (int kt = 0; kt < KT; kt += 2) {
+      // ---- stage kt (smem0) ----
+      read_slice(smem0, 1, opB, wn, wm, h, r32);
+      mfma_slice(opA, acc);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __syncthreads();  // every wave has read smem0
+      WANMI_GEMM_ISSUE(min(kt + 2, KT - 1), smem0);
+      __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage kt+1 (smem1) landed
+      __syncthreads();
+      read_slice(smem1, 0, opA, wn, wm, h, r32);
+      mfma_slice(opB, acc);
+      // ---- stage kt+1 (smem1) ----
+      read_slice(smem1, 1, opB, wn, wm, h, r32);
+      mfma_slice(opA, acc);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __syncthreads();  // every wave has read smem1
+      WANMI_GEMM_ISSUE(min(kt + 3, KT - 1), smem1);
+      __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage kt+2 (smem0) landed
+      __syncthreads();
+      read_slice(smem0, 0, opA, wn, wm, h, r32);  // past the last stage: a dead read
+      mfma_slice(opB, acc);
+    }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no load may still target LDS when the workgroup retires
 #undef WANMI_GEMM_ISSUE
 #undef WANMI_BLDS
 
@@ -361,6 +401,9 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   g.lda = lda;
   g.ldo = ldo;
   g.epilogue = epilogue;
-  hipLaunchKernelGGL(mxfp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, g);
+  if ((K / BK) % 2 == 0)
+    hipLaunchKernelGGL(mxfp8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, g);
+  else
+    hipLaunchKernelGGL(mxfp8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, g);
   return check_launch("wanmi_mxfp8_gemm");
 }
