@@ -50,3 +50,18 @@ extern "C" int wanmi_e4m3_encode(const float* in, uint8_t* out, int64_t n, void*
                      (hipStream_t)stream, in, out, n);
   return check_launch("wanmi_e4m3_encode");
 }
+
+namespace wanmi {
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
+}  // namespace wanmi

@@ -41,7 +41,6 @@ struct AdalnArgs {
   uint16_t* residual_out;
 };
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer descriptor word 3
 

@@ -22,7 +22,6 @@
 
 namespace wanmi {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kAttnRsrcWord3 = 0x00020000;
 constexpr int BQ = 128;  // queries per workgroup
 constexpr int BKV = 64;  // keys per tile
@@ -220,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a)
         y[r] = round_bf16(acc_o[dt][r] * inv);
         e = max(e, exp_field(y[r]));
       }
-      e = max(e, __shfl_xor(e, 32, 64));
+      e = max_with_lane_xor32(e);
       const int sx = max(e - 7, 0);
       const float f = mx_inv_scale(sx);
 #pragma unroll

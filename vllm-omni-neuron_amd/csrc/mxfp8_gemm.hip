@@ -14,13 +14,25 @@
 // (e4m3) vectors.
 //
 // Tiling: 256 (n) x 256 (m) x 128 (k) per workgroup of 4 waves, each wave a 128 x 128 block of
-// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand tiles are staged through LDS in two
+// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand codes are staged through LDS in two
 // stage buffers filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds, no VGPR round
 // trip), with a 16-byte-chunk XOR swizzle (chunk ^ (row & 7)) so the MFMA operand reads of eight
 // consecutive rows land on distinct banks. Each stage's loads are issued two stages ahead into the
 // buffer just consumed; operands are read per 64-deep slice into ping-pong registers so LDS reads
-// overlap the previous slice's MFMAs. Workgroup ids are remapped so each XCD (ids are
-// dealt round-robin over 8 XCDs) works on a contiguous, L2-friendly group of tiles.
+// overlap the previous slice's MFMAs. Block scales travel four stages at a time (16 bytes per row
+// in one load, double-buffered): a row's scale bytes are 4 bytes per stage, so per-stage loads
+// would cost an address-unit pass over 64 scattered rows for every 4 bytes.
+//
+// Measured on MI355X, these choices matter: direct-to-LDS loads with a non-zero scalar offset run
+// ~45% slower than with the whole offset in the VGPR, so row-group offsets live in VGPRs; and the
+// loads are issued from inline asm, invisible to the compiler's wait-count pass, which would
+// otherwise put a full vmcnt(0) before every LDS read and serialize the pipeline.
+//
+// The kernel is persistent: one workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ... in an
+// order where each XCD (workgroup ids are dealt round-robin over 8 XCDs) owns a contiguous,
+// L2-friendly run of tiles grouped 8 deep along m. The next tile's first two stages and its
+// epilogue vectors (bias, column/row scales, gate; staged in LDS) are loaded while the current
+// tile's epilogue runs, so the epilogue overlaps the next tile's load latency.
 //
 // Reference semantics: the ROW_MX projection epilogues of _qkv_cte_mx_impl / _dequant_row_mx
 // (vllm_omni_neuron/kernels/nkilib/core/qkv/qkv_cte.py:3711-3750, 3996-4021) and of the MLP
@@ -29,17 +41,19 @@
 // (kernels/nkilib/core/mlp/mlp_torch.py:401-599).
 #include "wanmi_common.h"
 
+#include <algorithm>
+
 namespace wanmi {
 
-constexpr int TN = 256;  // weight rows (output features) per workgroup
-constexpr int TM = 256;  // tokens per workgroup
+constexpr int TN = 256;  // weight rows (output features) per tile
+constexpr int TM = 256;  // tokens per tile
 constexpr int BK = 128;  // k bytes per stage (4 MX blocks)
-constexpr int kStageBytes = TN * BK + TM * BK + TN * 4 + TM * 4;
+constexpr int kStageBytes = TN * BK + TM * BK;  // e4m3 codes of one stage (W rows, then A rows)
+constexpr int kScaleGroup = 4;                    // stages per scale load (16 bytes per row)
+constexpr int kVecFloats = 4 * 256;  // per tile: bias[n], col_scale[n], gate[n], row_scale[m]
 constexpr int kGroupM = 8;
-constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw, 32-bit data)
-// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
-constexpr int kWaitVm18 = (18 & 0xF) | (0x7 << 4) | (0xF << 8) | ((18 >> 4) << 14);  // vmcnt <= 18
-constexpr int kWaitLgkm0 = 0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14);               // lgkmcnt == 0
+constexpr int kCodeLoads = 16;   // direct-to-LDS loads per wave per stage of codes (16 x 1 KiB)
+constexpr int kScaleLoads = 2;   // per wave per scale group (W rows, A rows; 16 B per row)
 
 struct GemmArgs {
   const uint8_t* a;         // [M, lda]
@@ -54,20 +68,19 @@ struct GemmArgs {
   void* out;                // [M, ldo]
   uint8_t* out_scales;      // [M, N/32]
   int64_t M, N, K, lda, ldo;
-  int epilogue;
+  int tiles_m, tiles_n;
 };
 
+// gelu_tanh(x) = 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3);
+// hardware exp2 and reciprocal (relative error ~1e-7, far below the bf16 rounding that follows).
+// Saturates correctly: exp(-2u) -> inf gives -0/+0, exp(-2u) -> 0 gives x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh via exp of -2|u|
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float t = __expf(-2.0f * fabsf(u));
-  float th = (1.0f - t) / (1.0f + t);
-  th = copysignf(th, u);
-  return 0.5f * x * (1.0f + th);
+  const float u = x * (0.7978845608028654f + 0.035677408136300125f * (x * x));
+  const float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);  // exp(-2u) = 2^(-2u log2 e)
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
-
 
 // MFMA operands of one 64-deep k slice of a wave's 128 x 128 block: 4 weight-row and 4 token-row
 // fragments (32 bytes per lane each) and their e8m0 scale bytes.
@@ -79,15 +92,20 @@ struct SliceOperands {
 };
 
 // Reads slice s (0 or 1) of an LDS stage. Lane data: bytes 0-15 = k[64s + 16h, +16),
-// bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of its row.
-__device__ __forceinline__ void read_slice(const uint8_t* base, int s, SliceOperands& op, int wn, int wm, int h,
-                                           int r32) {
+// bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of its row, in word q
+// (the stage's position in its scale group) of the row's 16 scale bytes in `sc` ([2][256] x 16 B:
+// W rows, then A rows).
+__device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& op,
+                                           int wn, int wm, int h, int r32) {
   const uint8_t* sw = base;
   const uint8_t* sa = base + TN * BK;
-  const uint32_t* sws = reinterpret_cast<const uint32_t*>(base + TN * BK + TM * BK);
-  const uint32_t* sas = sws + TN;
   const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
   const int sh = 8 * (2 * s + h);
+  // scale-word addresses from a freshly computed lane id: held across the loop they would be one
+  // more set of long-lived VGPRs per scale buffer and word, which the allocator spills
+  const int fr = fresh_lane_id() & 31;
+  const uint32_t* scw = sc + (wn * 128 + fr) * 4 + q;
+  const uint32_t* sca = sc + (TN + wm * 128 + fr) * 4 + q;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int rw = wn * 128 + i * 32 + r32;
@@ -98,55 +116,167 @@ __device__ __forceinline__ void read_slice(const uint8_t* base, int s, SliceOper
     const uint4 y0 = *reinterpret_cast<const uint4*>(sa + swz(ra, c0));
     const uint4 y1 = *reinterpret_cast<const uint4*>(sa + swz(ra, c1));
     op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
-    op.ws[i] = (int)((sws[rw] >> sh) & 0xFFu);
-    op.as[i] = (int)((sas[ra] >> sh) & 0xFFu);
+    op.ws[i] = (int)((scw[i * 32 * 4] >> sh) & 0xFFu);
+    op.as[i] = (int)((sca[i * 32 * 4] >> sh) & 0xFFu);
   }
 }
 
-__device__ __forceinline__ void mfma_slice(const SliceOperands& op, f32x16 (&acc)[4][4]) {
+// MFMAs of weight-row fragments [I0, I1) against all four token fragments.
+template <int I0, int I1>
+__device__ __forceinline__ void mfma_rows(const SliceOperands& op, f32x16 (&acc)[4][4]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = I0; i < I1; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
                                                                    op.as[j]);
 }
 
-// One 32 x 32 accumulator tile: lane holds token m and n = ntile + 8*gi + 4*h + q (gi, q in 0..3).
+// Per-tile buffer resources of one wave's direct-to-LDS loads.
+struct TileLoads {
+  u32x4 w, a, ws, as;
+  int64_t m0, n0, m_valid;
+};
+
+__device__ __forceinline__ void tile_coords(const GemmArgs& g, int v, int64_t& m0, int64_t& n0) {
+  const int total = g.tiles_m * g.tiles_n;
+  int pid = v;
+  if ((total & 7) == 0) pid = (v & 7) * (total >> 3) + (v >> 3);
+  const int in_group = kGroupM * g.tiles_n;
+  const int group = pid / in_group;
+  const int first_m = group * kGroupM;
+  const int gsz = min(g.tiles_m - first_m, kGroupM);
+  const int tm = first_m + (pid % in_group) % gsz;
+  const int tn = (pid % in_group) / gsz;
+  n0 = (int64_t)tn * TN;
+  m0 = (int64_t)tm * TM;
+}
+
+__device__ __forceinline__ TileLoads tile_loads(const GemmArgs& g, int v) {
+  TileLoads t;
+  tile_coords(g, v, t.m0, t.n0);
+  const int64_t KB = g.K / 32;
+  t.m_valid = min((int64_t)TM, g.M - t.m0);
+  // Token rows past M fall outside the activation resources' extent and read as zero.
+  t.w = buffer_rsrc(g.w + t.n0 * g.K, (uint32_t)(TN * g.K));
+  t.a = buffer_rsrc(g.a + t.m0 * g.lda, (uint32_t)(t.m_valid * g.lda));
+  t.ws = buffer_rsrc(g.w_scales + t.n0 * KB, (uint32_t)(TN * KB));
+  t.as = buffer_rsrc(g.a_scales + t.m0 * KB, (uint32_t)(t.m_valid * KB));
+  return t;
+}
+
+// Codes of stage kt -> LDS stage buffer `buf`. Wave w fills rows 64w .. 64w+63 of each operand
+// tile, 8 rows (1 KiB) per instruction: lane l lands in physical 16-byte slot l & 7 of row
+// 8i + (l >> 3) and fetches the logical chunk the XOR swizzle assigns to that slot. One asm block
+// steps M0 (the LDS destination) and two VGPR offsets itself (every M0 write is followed by
+// another instruction before the load that reads it); the scalar offset stays 0.
+#define WANMI_DMA_ROW_PAIR                                   \
+  "buffer_load_dwordx4 %[tw], %[rw], 0 offen lds\n\t"        \
+  "s_add_u32 m0, m0, 0x8000\n\t"                             \
+  "v_add_u32 %[tw], %[wstep], %[tw]\n\t"                     \
+  "buffer_load_dwordx4 %[ta], %[ra], 0 offen lds\n\t"        \
+  "s_add_u32 m0, m0, 0xffff8400\n\t"                         \
+  "v_add_u32 %[ta], %[astep], %[ta]\n\t"
+static_assert(TN * BK == 0x8000 && 8 * BK - TN * BK == -0x7c00,
+              "M0 steps in the stage DMA assume 32 KiB operand tiles and 1 KiB row groups");
+
+// !valid: an empty extent turns every load into a zero fill that moves no memory (branch-free)
+__device__ __forceinline__ u32x4 maybe_empty(u32x4 r, bool valid) {
+  r[2] = valid ? r[2] : 0u;
+  return r;
+}
+
+__device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
+                                            uint32_t voff_w, uint32_t voff_a, bool valid = true) {
+  const u32x4 rw = maybe_empty(t.w, valid), ra = maybe_empty(t.a, valid);
+  const uint32_t k0 = (uint32_t)kt * BK;
+  const uint32_t vw = voff_w + (uint32_t)(wave * 64 * g.K) + k0;
+  const uint32_t va = voff_a + (uint32_t)(wave * 64 * g.lda) + k0;
+  const uint32_t wstep = (uint32_t)(8 * g.K), astep = (uint32_t)(8 * g.lda);
+  const uint32_t lw = lds_addr(buf) + wave * 64 * BK;
+  uint32_t tw, ta;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile(
+      "s_mov_b32 m0, %[lw]\n\t"
+      "v_mov_b32 %[tw], %[vw]\n\t"
+      "v_mov_b32 %[ta], %[va]\n\t"
+      WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR
+      WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR
+      : [tw] "=&v"(tw), [ta] "=&v"(ta)
+      : [vw] "v"(vw), [va] "v"(va), [rw] "s"(rw), [ra] "s"(ra), [wstep] "s"(wstep), [astep] "s"(astep), [lw] "s"(lw)
+      : "memory", "m0", "scc");
+#pragma clang diagnostic pop
+}
+#undef WANMI_DMA_ROW_PAIR
+
+// Scale bytes of stage group grp (stages 4 grp .. 4 grp + 3, k-blocks [16 grp, 16 grp + 16)) ->
+// `sc` ([2][256] x 16 B). Lane l of wave w copies the 16 bytes of row 64w + l of each operand.
+__device__ __forceinline__ void issue_scales(const GemmArgs& g, const TileLoads& t, int grp, uint32_t* sc, int wave,
+                                             bool valid = true) {
+  const uint32_t KB = (uint32_t)(g.K / 32);
+  const uint32_t v = (uint32_t)(wave * 64 + fresh_lane_id()) * KB + (uint32_t)grp * 16;
+  const uint32_t ls = lds_addr(sc) + wave * 64 * 16;
+  lds_dma_b128(maybe_empty(t.ws, valid), v, ls);
+  lds_dma_b128(maybe_empty(t.as, valid), v, ls + TN * 16);
+}
+
+// The tile's epilogue vectors -> LDS (floats [0,256) bias, [256,512) col_scale, [512,768) gate,
+// [768,1024) row_scale). Absent vectors are not loaded: their LDS slots keep the neutral values
+// written once by init_vectors.
+__device__ __forceinline__ void issue_vectors(const GemmArgs& g, const TileLoads& t, float* vec, int wave) {
+  const uint32_t voff = (uint32_t)fresh_lane_id() * 4;
+  const uint32_t soff = (uint32_t)wave * 64 * 4;
+  const uint32_t base = lds_addr(vec) + wave * 64 * 4;
+  if (g.bias) lds_dma_b32(buffer_rsrc(g.bias + t.n0, TN * 4), voff, soff, base);
+  if (g.col_scale) lds_dma_b32(buffer_rsrc(g.col_scale + t.n0, TN * 4), voff, soff, base + 256 * 4);
+  if (g.gate) lds_dma_b32(buffer_rsrc(g.gate + t.n0, TN * 4), voff, soff, base + 512 * 4);
+  if (g.row_scale) lds_dma_b32(buffer_rsrc(g.row_scale + t.m0, (uint32_t)(t.m_valid * 4)), voff, soff, base + 768 * 4);
+}
+
+// Neutral values for the absent epilogue vectors, in both LDS vector buffers: bias -0 (x + -0 == x
+// for every x, signed zeros included) and scale 1.
+__device__ __forceinline__ void init_vectors(const GemmArgs& g, float (*svec)[kVecFloats], int tid) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (!g.bias) svec[b][tid] = -0.0f;
+    if (!g.col_scale) svec[b][256 + tid] = 1.0f;
+    if (!g.gate) svec[b][512 + tid] = 1.0f;
+    if (!g.row_scale) svec[b][768 + tid] = 1.0f;
+  }
+}
+
+// One 32 x 32 accumulator tile: lane holds token m and n = nt + 8*gi + 4*h + q (gi, q in 0..3);
+// nt, mt are the tile's offsets inside the workgroup tile (vector indices in LDS).
 template <int EPI>
-__device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a, int64_t m, int64_t ntile,
-                                              int h) {
+__device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a, const float* vec, int m,
+                                              int n0, int nt, int mt, int h, const uint2* res) {
 #pragma clang fp contract(off)
-  const bool mok = m < g.M;
-  const float rsc = (g.row_scale && mok) ? g.row_scale[m] : 1.0f;
+  const bool mok = m < (int)g.M;
+  const uint32_t row = (uint32_t)m * (uint32_t)g.ldo;  // element offset of the lane's output row (< 2^32)
+  // absent vectors hold their neutral values (bias -0, scales 1), so this is exact without them
+  const float rsc = vec[768 + mt];
   float v[16];
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi) {
-    const int64_t nb = ntile + gi * 8 + h * 4;
-    float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (g.bias) b = *reinterpret_cast<const float4*>(g.bias + nb);
-    float4 cs = make_float4(1.f, 1.f, 1.f, 1.f);
-    if (g.col_scale) cs = *reinterpret_cast<const float4*>(g.col_scale + nb);
+    const int nl = nt + gi * 8 + h * 4;
+    const float4 b = *reinterpret_cast<const float4*>(vec + nl);
+    const float4 cs = *reinterpret_cast<const float4*>(vec + 256 + nl);
     const float bb[4] = {b.x, b.y, b.z, b.w};
     const float cc[4] = {cs.x, cs.y, cs.z, cs.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float x = a[gi * 4 + q];
-      if (g.row_scale) x = x * rsc;
-      if (g.col_scale) x = x * cc[q];
-      v[gi * 4 + q] = x + bb[q];
-    }
+    for (int q = 0; q < 4; ++q) v[gi * 4 + q] = (a[gi * 4 + q] * rsc) * cc[q] + bb[q];
   }
   if constexpr (EPI == WANMI_EPI_BF16 || EPI == WANMI_EPI_GELU_BF16) {
     uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const int64_t nb = ntile + gi * 8 + h * 4;
+      const uint32_t nb = (uint32_t)(n0 + nt + gi * 8 + h * 4);
       float y[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) y[q] = EPI == WANMI_EPI_GELU_BF16 ? gelu_tanh(v[gi * 4 + q]) : v[gi * 4 + q];
       if (mok)
-        *reinterpret_cast<uint2*>(out + m * g.ldo + nb) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        *reinterpret_cast<uint2*>(out + (row + nb)) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
     }
   } else if constexpr (EPI == WANMI_EPI_GELU_MX) {
     float y[16];
@@ -156,25 +286,24 @@ __device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a
       y[q] = round_bf16(gelu_tanh(v[q]));
       e = max(e, exp_field(y[q]));
     }
-    e = max(e, __shfl_xor(e, 32, 64));  // lanes l and l^32 hold the two halves of the 32-block
+    e = max_with_lane_xor32(e);  // lanes l and l^32 hold the two halves of the 32-block
     const int s = max(e - 7, 0);
     const float f = mx_inv_scale(s);
     uint8_t* codes = reinterpret_cast<uint8_t*>(g.out);
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const int64_t nb = ntile + gi * 8 + h * 4;
+      const uint32_t nb = (uint32_t)(n0 + nt + gi * 8 + h * 4);
       const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
-      if (mok) *reinterpret_cast<uint32_t*>(codes + m * g.ldo + nb) = c4;
+      if (mok) *reinterpret_cast<uint32_t*>(codes + (row + nb)) = c4;
     }
-    if (mok && h == 0) g.out_scales[m * (g.N / 32) + ntile / 32] = (uint8_t)s;
+    if (mok && h == 0) g.out_scales[(uint32_t)m * (uint32_t)(g.N / 32) + (uint32_t)((n0 + nt) / 32)] = (uint8_t)s;
   } else {  // gated residual: out = bf16(res + bf16(v) * gate)
     uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const int64_t nb = ntile + gi * 8 + h * 4;
-      if (!mok) continue;
-      const uint2 r = *reinterpret_cast<const uint2*>(g.residual + m * g.ldo + nb);
-      const float4 gt = *reinterpret_cast<const float4*>(g.gate + nb);
+      const int nl = nt + gi * 8 + h * 4;
+      const uint2 r = res[gi];
+      const float4 gt = *reinterpret_cast<const float4*>(vec + 512 + nl);
       const float rr[4] = {bf16_lo(r.x), bf16_hi(r.x), bf16_lo(r.y), bf16_hi(r.y)};
       const float gg[4] = {gt.x, gt.y, gt.z, gt.w};
       float y[4];
@@ -184,165 +313,190 @@ __device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a
         const float prod = f * gg[q];
         y[q] = rr[q] + prod;
       }
-      *reinterpret_cast<uint2*>(out + m * g.ldo + nb) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+      if (mok) *reinterpret_cast<uint2*>(out + (row + (uint32_t)(n0 + nl))) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
     }
   }
 }
 
-template <int EPI, int I = 0>
-__device__ __forceinline__ void epilogue_all(const GemmArgs& g, const f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
-                                             int wm, int wn, int lane) {
-  if constexpr (I < 16) {
-    constexpr int i = I / 4, j = I % 4;
-    epilogue_tile<EPI>(g, acc[i][j], m0 + wm * 128 + j * 32 + (lane & 31), n0 + wn * 128 + i * 32, lane >> 5);
-    epilogue_all<EPI, I + 1>(g, acc, m0, n0, wm, wn, lane);
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec, int m0, int n0,
+                                         int wm, int wn, int lane) {
+  const int h = lane >> 5;
+  if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) {
+    // all 64 residual loads of the wave first (one latency), then the arithmetic
+    uint2 res[4][4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + wm * 128 + j * 32 + (lane & 31);
+      const bool mok = m < (int)g.M;
+      const uint32_t row = (uint32_t)m * (uint32_t)g.ldo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const uint32_t nb = (uint32_t)(n0 + wn * 128 + i * 32 + gi * 8 + h * 4);
+          res[i][j][gi] = mok ? *reinterpret_cast<const uint2*>(g.residual + (row + nb)) : make_uint2(0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        epilogue_tile<EPI>(g, acc[i][j], vec, m0 + wm * 128 + j * 32 + (lane & 31), n0, wn * 128 + i * 32,
+                           wm * 128 + j * 32 + (lane & 31), h, res[i][j]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        epilogue_tile<EPI>(g, acc[i][j], vec, m0 + wm * 128 + j * 32 + (lane & 31), n0, wn * 128 + i * 32,
+                           wm * 128 + j * 32 + (lane & 31), h, nullptr);
+        // one accumulator tile at a time: interleaving tiles raises register pressure into spills,
+        // and a spill reload would wait for the next tile's in-flight loads
+        __builtin_amdgcn_sched_barrier(0);
+      }
   }
 }
 
-// kEvenStages: the pipelined, branch-free loop below (K a multiple of 256); otherwise a simple
-// double-buffered loop that issues the next stage's loads after all reads of the current one.
-template <bool kEvenStages>
+// kPipelined: the pipelined main loop (K a multiple of 512: whole scale groups, stage pairs);
+// otherwise a simple double-buffered loop that issues the next stage's loads after all reads of the
+// current one.
+template <bool kPipelined, int EPI>
 __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
-  // Two separate LDS objects: the compiler can then prove that the stage being read never aliases
-  // the stage being filled by in-flight direct-to-LDS loads, and waits only on the latter's own.
   __shared__ __attribute__((aligned(16))) uint8_t smem0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t smem1[kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t ssc[2][2 * 256 * 4];  // scale groups, double-buffered
+  __shared__ __attribute__((aligned(16))) float svec[2][kVecFloats];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave >> 1, wm = wave & 1;
-  const int64_t M = g.M, N = g.N, K = g.K;
-  const int KB = (int)(K / 32);
-
-  // ---- tile mapping: XCD-contiguous chunks, grouped along m ----
-  const int tiles_n = (int)(N / TN);
-  const int tiles_m = (int)((M + TM - 1) / TM);
-  const int total = tiles_n * tiles_m;
-  int pid = blockIdx.x;
-  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
-  const int in_group = kGroupM * tiles_n;
-  const int group = pid / in_group;
-  const int first_m = group * kGroupM;
-  const int gsz = min(tiles_m - first_m, kGroupM);
-  const int tm = first_m + (pid % in_group) % gsz;
-  const int tn = (pid % in_group) / gsz;
-  const int64_t n0 = (int64_t)tn * TN, m0 = (int64_t)tm * TM;
-
-  // ---- global -> LDS staging: buffer loads straight into LDS (no VGPR round trip) ----
-  // Wave w fills rows 64w .. 64w+63 of each operand tile, 8 rows (1 KiB) per instruction: lane l
-  // lands in physical 16-byte slot l & 7 of row 8i + (l >> 3) and fetches the logical chunk the XOR
-  // swizzle assigns to that slot. Token rows past M fall outside the activation buffer resource's
-  // extent and read as zero (they are never stored).
-  const int srow = lane >> 3;
-  const int schunk = (lane & 7) ^ (srow & 7);
-  const int64_t m_valid = min((int64_t)TM, M - m0);
-  const __amdgpu_buffer_rsrc_t rs_w =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(g.w + n0 * K), (short)0, (int)(TN * K), kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rs_a =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + m0 * g.lda), (short)0, (int)(m_valid * g.lda), kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rs_ws =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(g.w_scales + n0 * KB), (short)0, TN * KB, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rs_as =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(g.a_scales + m0 * KB), (short)0, (int)(m_valid * KB), kBufferRsrcWord3);
-  const uint32_t voff_w = (uint32_t)((wave * 64 + srow) * K + schunk * 16);
-  const uint32_t voff_a = (uint32_t)((wave * 64 + srow) * g.lda + schunk * 16);
-  const uint32_t voff_s = (uint32_t)((wave * 64 + lane) * KB);
-  const uint32_t wstep = (uint32_t)(8 * K), astep = (uint32_t)(8 * g.lda);
-
-#define WANMI_BLDS(rs, dst, bytes, voff) \
-  __builtin_amdgcn_raw_ptr_buffer_load_lds((rs), (__attribute__((address_space(3))) void*)(dst), (bytes), (voff), 0, 0, 0)
-
-#define WANMI_GEMM_ISSUE(kt, buf)                                                                \
-  do {                                                                                           \
-    const uint32_t k0_ = (uint32_t)(kt) * BK;                                                    \
-    uint8_t* base_ = (buf) + wave * 64 * BK;                                                     \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                              \
-      WANMI_BLDS(rs_w, base_ + i * 8 * BK, 16, voff_w + i * wstep + k0_);                         \
-      WANMI_BLDS(rs_a, base_ + TN * BK + i * 8 * BK, 16, voff_a + i * astep + k0_);               \
-    }                                                                                            \
-    uint8_t* sbase_ = (buf) + TN * BK + TM * BK + wave * 64 * 4;                                 \
-    WANMI_BLDS(rs_ws, sbase_, 4, voff_s + (kt) * 4);                                             \
-    WANMI_BLDS(rs_as, sbase_ + TN * 4, 4, voff_s + (kt) * 4);                                    \
-  } while (0)
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int KT = (int)(K / BK);
   const int h = lane >> 5;
   const int r32 = lane & 31;
+  const int KT = (int)(g.K / BK);
+  const int total = g.tiles_m * g.tiles_n;
+  // lane parts of the DMA offsets (the same for every tile and stage)
+  const int srow = lane >> 3;
+  const int schunk = (lane & 7) ^ (srow & 7);
+  const uint32_t voff_w = (uint32_t)(srow * g.K + schunk * 16);
+  const uint32_t voff_a = (uint32_t)(srow * g.lda + schunk * 16);
+  // Prefetching the next tile before the epilogue would make the gated-residual epilogue's own
+  // residual loads wait behind those loads (the wait counter is in order), so that epilogue
+  // prefetches after.
+  constexpr bool kPrefetchBeforeEpilogue = EPI != WANMI_EPI_GATED_RESIDUAL;
 
-  if constexpr (!kEvenStages) {
-    // stage kt in smem0 / smem1 alternately; the next stage's loads go into the other buffer
-    // (read by nobody since the previous barrier) before this stage's MFMAs
-    WANMI_GEMM_ISSUE(0, smem0);
-    __builtin_amdgcn_s_waitcnt(0);
+  auto prefetch = [&](const TileLoads& tl, float* vec) {
+    issue_vectors(g, tl, vec, wave);
+    issue_scales(g, tl, 0, ssc[0], wave);
+    issue_codes(g, tl, 0, smem0, wave, voff_w, voff_a);
+    if constexpr (kPipelined) issue_codes(g, tl, 1, smem1, wave, voff_w, voff_a);
+  };
+
+  int v = blockIdx.x;
+  init_vectors(g, svec, tid);  // published by the barrier at the top of the tile loop
+  prefetch(tile_loads(g, v), svec[0]);
+  int vb = 0;
+
+  f32x16 acc[4][4];
+  for (;;) {
+    // tile state is recomputed per tile (cheap scalar work) rather than carried across the epilogue
+    const TileLoads t = tile_loads(g, v);
+    __builtin_amdgcn_s_waitcnt(0);  // this tile's first stages, scales and vectors have landed
     __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      uint8_t* cur = (kt & 1) ? smem1 : smem0;
-      uint8_t* nxt = (kt & 1) ? smem0 : smem1;
-      if (kt + 1 < KT) WANMI_GEMM_ISSUE(kt + 1, nxt);
-      SliceOperands op;
-      read_slice(cur, 0, op, wn, wm, h, r32);
-      mfma_slice(op, acc);
-      read_slice(cur, 1, op, wn, wm, h, r32);
-      mfma_slice(op, acc);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if constexpr (!kPipelined) {
+      for (int kt = 0; kt < KT; ++kt) {
+        uint8_t* cur = (kt & 1) ? smem1 : smem0;
+        uint8_t* nxt = (kt & 1) ? smem0 : smem1;
+        const uint32_t* sc = ssc[(kt / kScaleGroup) & 1];
+        // nobody reads nxt, nor the other scale buffer, since the last barrier
+        if (kt + 1 < KT) {
+          if ((kt + 1) % kScaleGroup == 0) issue_scales(g, t, (kt + 1) / kScaleGroup, ssc[((kt + 1) / kScaleGroup) & 1], wave);
+          issue_codes(g, t, kt + 1, nxt, wave, voff_w, voff_a);
+        }
+        SliceOperands op;
+        read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32);
+        mfma_rows<0, 4>(op, acc);
+        read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32);
+        mfma_rows<0, 4>(op, acc);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    } else {
+      // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], word
+      // s % 4. Per stage: the slice-0 MFMAs run while slice 1 is read; a barrier (every wave has
+      // read the stage) lets the loads of stage s+2 go into the same buffer during the first half
+      // of the slice-1 MFMAs; a second barrier (every wave's stage s+1 has landed) lets slice 0 of
+      // stage s+1 be read during the second half. The scales of group g+1 are loaded with stage
+      // 4g+4's codes. The body has no branches (conditional issue makes the register allocator
+      // spill operands): in the last iteration the loads past the end are issued against an empty
+      // resource, which moves no data and zero-fills buffers nobody reads again, and the slice
+      // read after the final barrier is dead.
+#define WANMI_GEMM_STAGE(S, CUR, OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                     \
+  do {                                                                                             \
+    read_slice(CUR, SC_CUR, Q_CUR, 1, opB, wn, wm, h, r32);                                        \
+    mfma_rows<0, 4>(opA, acc);                                                                     \
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                   \
+    __syncthreads(); /* every wave has read CUR */                                                 \
+    const bool more_ = (S) + 2 < KT;                                                               \
+    if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
+    issue_codes(g, t, more_ ? (S) + 2 : 0, CUR, wave, voff_w, voff_a, more_);                      \
+    mfma_rows<0, 2>(opB, acc);                                                                     \
+    /* stage S+1 landed: only stage S+2's loads may still be in flight */                         \
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((WITH_SCALES) ? kCodeLoads + kScaleLoads : kCodeLoads));  \
+    __syncthreads();                                                                               \
+    read_slice(OTH, SC_NXT, Q_NXT, 0, opA, wn, wm, h, r32);                                        \
+    mfma_rows<2, 4>(opB, acc);                                                                     \
+  } while (0)
+
+      SliceOperands opA, opB;
+      read_slice(smem0, ssc[0], 0, 0, opA, wn, wm, h, r32);
+      for (int kt = 0; kt < KT; kt += 4) {
+        const int sg = (kt / kScaleGroup) & 1;  // this group's scale buffer; the next group's is sg ^ 1
+        WANMI_GEMM_STAGE(kt, smem0, smem1, ssc[sg], 0, ssc[sg], 1, false);
+        WANMI_GEMM_STAGE(kt + 1, smem1, smem0, ssc[sg], 1, ssc[sg], 2, false);
+        WANMI_GEMM_STAGE(kt + 2, smem0, smem1, ssc[sg], 2, ssc[sg], 3, true);
+        WANMI_GEMM_STAGE(kt + 3, smem1, smem0, ssc[sg], 3, ssc[sg ^ 1], 0, false);
+      }
+#undef WANMI_GEMM_STAGE
     }
-  } else {
-    // Pipeline (KT even, branch-free): stage kt lives in smem0 for even kt, smem1 for odd kt. The
-    // loads of stage kt+2 go into the buffer stage kt was just read from (after a barrier confirms
-    // every wave has read it), so each stage's loads have two stages of MFMA work to land; past the
-    // end the stage index is clamped, re-loading the last stage into a buffer nobody reads again.
-    // Within a stage the two 64-deep slices are read into ping-pong registers, each slice's LDS
-    // reads overlapping the previous slice's MFMAs.
-    WANMI_GEMM_ISSUE(0, smem0);
-    WANMI_GEMM_ISSUE(1, smem1);
-    __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage 0 landed (stage 1's 18 loads may be in flight)
-    __syncthreads();
-    SliceOperands opA, opB;
-    read_slice(smem0, 0, opA, wn, wm, h, r32);
-    for (int kt = 0; kt < KT; kt += 2) {
-      // ---- stage kt (smem0) ----
-      read_slice(smem0, 1, opB, wn, wm, h, r32);
-      mfma_slice(opA, acc);
-      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      __syncthreads();  // every wave has read smem0
-      WANMI_GEMM_ISSUE(min(kt + 2, KT - 1), smem0);
-      __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage kt+1 (smem1) landed
+
+    // Every wave is past its last LDS operand read of this tile (the last barrier above follows
+    // them), so the stage buffers may be refilled with the next tile.
+    const int m0 = (int)t.m0, n0 = (int)t.n0;
+    const int vn = v + (int)gridDim.x;
+    const bool has_next = vn < total;
+    if (kPrefetchBeforeEpilogue && has_next) {
       __syncthreads();
-      read_slice(smem1, 0, opA, wn, wm, h, r32);
-      mfma_slice(opB, acc);
-      // ---- stage kt+1 (smem1) ----
-      read_slice(smem1, 1, opB, wn, wm, h, r32);
-      mfma_slice(opA, acc);
-      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      __syncthreads();  // every wave has read smem1
-      WANMI_GEMM_ISSUE(min(kt + 3, KT - 1), smem1);
-      __builtin_amdgcn_s_waitcnt(kWaitVm18);  // stage kt+2 (smem0) landed
-      __syncthreads();
-      read_slice(smem0, 0, opA, wn, wm, h, r32);  // past the last stage: a dead read
-      mfma_slice(opB, acc);
+      prefetch(tile_loads(g, vn), svec[vb ^ 1]);
     }
+    epilogue<EPI>(g, acc, svec[vb], m0, n0, wm, wn, fresh_lane_id());
+    if (!kPrefetchBeforeEpilogue && has_next) {
+      __syncthreads();
+      prefetch(tile_loads(g, vn), svec[vb ^ 1]);
+    }
+    if (!has_next) break;
+    v = vn;
+    vb ^= 1;
   }
   __builtin_amdgcn_s_waitcnt(0);  // no load may still target LDS when the workgroup retires
-#undef WANMI_GEMM_ISSUE
-#undef WANMI_BLDS
+}
 
-  // ---- epilogue (expanded per tile and per epilogue kind, so accumulator indices are static) ----
-  switch (g.epilogue) {
-    case WANMI_EPI_BF16: epilogue_all<WANMI_EPI_BF16>(g, acc, m0, n0, wm, wn, lane); break;
-    case WANMI_EPI_GELU_MX: epilogue_all<WANMI_EPI_GELU_MX>(g, acc, m0, n0, wm, wn, lane); break;
-    case WANMI_EPI_GELU_BF16: epilogue_all<WANMI_EPI_GELU_BF16>(g, acc, m0, n0, wm, wn, lane); break;
-    default: epilogue_all<WANMI_EPI_GATED_RESIDUAL>(g, acc, m0, n0, wm, wn, lane); break;
+template <bool kEven>
+static void launch_gemm(int epilogue, dim3 grid, hipStream_t stream, const GemmArgs& g) {
+  switch (epilogue) {
+    case WANMI_EPI_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_BF16>), grid, dim3(256), 0, stream, g); break;
+    case WANMI_EPI_GELU_MX: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_MX>), grid, dim3(256), 0, stream, g); break;
+    case WANMI_EPI_GELU_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_BF16>), grid, dim3(256), 0, stream, g); break;
+    default: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GATED_RESIDUAL>), grid, dim3(256), 0, stream, g); break;
   }
 }
 
@@ -382,6 +536,11 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
                 WANMI_ERR_ARG, "wanmi_mxfp8_gemm: misaligned operand");
   const int64_t tiles = (N / TN) * ((M + TM - 1) / TM);
   WANMI_REQUIRE(tiles < (1LL << 31), WANMI_ERR_ARG, "wanmi_mxfp8_gemm: problem too large");
+  WANMI_REQUIRE(M * ldo < (1LL << 32) && M < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+                "wanmi_mxfp8_gemm: M=%lld x ldo=%lld output elements exceed 32-bit offsets", (long long)M, (long long)ldo);
+  // per-tile buffer offsets are 32-bit
+  WANMI_REQUIRE(TN * K < (1LL << 31) && TM * lda < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+                "wanmi_mxfp8_gemm: K=%lld / lda=%lld too large", (long long)K, (long long)lda);
 
   GemmArgs g;
   g.a = a_codes;
@@ -392,7 +551,7 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   g.col_scale = col_scale;
   g.bias = bias;
   g.residual = static_cast<const uint16_t*>(residual);
-  g.gate = gate;
+  g.gate = epilogue == WANMI_EPI_GATED_RESIDUAL ? gate : nullptr;
   g.out = out;
   g.out_scales = out_scales;
   g.M = M;
@@ -400,10 +559,15 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   g.K = K;
   g.lda = lda;
   g.ldo = ldo;
-  g.epilogue = epilogue;
-  if ((K / BK) % 2 == 0)
-    hipLaunchKernelGGL(mxfp8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, g);
+  g.tiles_m = (int)((M + TM - 1) / TM);
+  g.tiles_n = (int)(N / TN);
+  // persistent: one workgroup per CU (the LDS footprint allows no second one)
+  const int cus = device_cu_count();
+  WANMI_REQUIRE(cus > 0, WANMI_ERR_HIP, "wanmi_mxfp8_gemm: cannot query the device's compute units");
+  const dim3 grid((unsigned)std::min<int64_t>(tiles, cus));
+  if ((K / BK) % 4 == 0)
+    launch_gemm<true>(epilogue, grid, (hipStream_t)stream, g);
   else
-    hipLaunchKernelGGL(mxfp8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, g);
+    launch_gemm<false>(epilogue, grid, (hipStream_t)stream, g);
   return check_launch("wanmi_mxfp8_gemm");
 }

@@ -19,7 +19,6 @@
 
 namespace wanmi {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {

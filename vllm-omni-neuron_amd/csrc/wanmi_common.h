@@ -30,6 +30,9 @@ void clear_error();
 // Checks the launch that was just issued (configuration errors surface synchronously).
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device); 0 if the query fails.
+int device_cu_count();
+
 // ------------------------------------------------------------------------------------------------
 // Device: vector types and bit helpers
 // ------------------------------------------------------------------------------------------------
@@ -69,6 +72,65 @@ __device__ __forceinline__ uint32_t cvt_e4m3x4(float a, float b, float c, float 
   r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
   return (uint32_t)r;
 }
+
+// ------------------------------------------------------------------------------------------------
+// Device: buffer descriptors and direct-to-LDS loads
+// ------------------------------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// gfx9 buffer resource in four SGPRs: 48-bit base, stride 0, extent in bytes (loads at offsets at
+// or past it return zero), raw 32-bit data format.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+// Byte address of a __shared__ object inside the workgroup's LDS allocation.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Direct-to-LDS loads: lane l copies 16 (or 4) bytes from rsrc + voff to LDS address lds + 16 l
+// (4 l); `lds` must be wave-uniform. They are issued as inline asm so that the compiler's wait-count
+// pass does not see them: it cannot tell which LDS bytes an in-flight DMA writes, and would make
+// every later LDS read wait for all outstanding loads (vmcnt(0)), which serializes a multi-stage
+// pipeline. The caller therefore waits explicitly (s_waitcnt vmcnt(n) for its own loads, then a
+// barrier) before any wave reads the destination.
+__device__ __forceinline__ void lds_dma_b128(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma_b32(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+// The same with a wave-uniform byte offset `soff` (an SGPR) added to every lane's `voff`, so that
+// per-stage and per-row-group offsets cost no VGPRs.
+__device__ __forceinline__ void lds_dma_b128(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma_b32(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+}
+
+// Lane index recomputed on the spot (volatile, so not merged with earlier copies): code that runs
+// after a register-heavy loop derives its lane-dependent addresses from this instead of keeping
+// them live (and spilled) across the loop.
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// max(x[l], x[l ^ 32]) in every lane l, with v_permlane32_swap (which exchanges one 32-lane half of
+// its two operands): passing x as both operands, the two results hold x[l] and x[l ^ 32] in some
+// order, so their max is the pair max whichever half the instruction swaps. No LDS, no lane id.
+__device__ __forceinline__ int max_with_lane_xor32(int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14)
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+constexpr int waitcnt_lgkm(int n) { return 0xF | (0x7 << 4) | ((n & 0xF) << 8) | (0x3 << 14); }
 
 // Wavefront (64-lane) reductions via cross-lane shuffles.
 __device__ __forceinline__ int wave_max_i32(int v) {
