@@ -23,8 +23,11 @@
 namespace wanmi {
 
 constexpr int kAttnRsrcWord3 = 0x00020000;
-constexpr int BQ = 128;  // queries per workgroup
-constexpr int BKV = 64;  // keys per tile
+constexpr int kWaves = 8;          // waves per workgroup, 32 queries each
+constexpr int BQ = 32 * kWaves;    // queries per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int BKV = 64;            // keys per LDS tile (two 32-key halves)
+constexpr int kStages = 4;         // LDS ring depth in tiles
 constexpr float kSumFloor = 1e-37f;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* p, int64_t bytes) {
@@ -50,19 +53,91 @@ struct AttnArgs {
   int64_t os_ss;
 };
 
-// LDS tiles (single-buffered; 2 workgroups per CU overlap each other's loads and compute).
+// LDS tiles, a ring of kStages (tile t in slot t % kStages):
 //   sK: [64 keys][128 d] bf16, 16-byte chunk index XOR (key & 15)
 //   sV: [128 d][64 slots] bf16, 16-byte chunk index XOR (d & 7)
 __device__ __forceinline__ int sk_off(int key, int chunk) { return key * 256 + ((chunk ^ (key & 15)) << 4); }
 __device__ __forceinline__ int sv_off(int d, int chunk) { return d * 128 + ((chunk ^ (d & 7)) << 4); }
+constexpr int kTileK = BKV * 256;      // bytes of one K tile
+constexpr int kTileV = 128 * BKV * 2;  // bytes of one V^T tile
+constexpr int kLoadsPerTile = 4;       // direct-to-LDS instructions per wave per tile (2 K + 2 V)
+
+// S^T of one 32-key half (keys 32 i .. 32 i + 31 of the LDS tile) against the wave's 32 queries:
+// 8 MFMAs over d, K fragments read ahead of the chain.
+__device__ __forceinline__ f32x16 qk_half(const uint8_t* cK, int i, const bf16x8 (&qf)[8], int col, int hq) {
+  bf16x8 kf[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) kf[t] = *reinterpret_cast<const bf16x8*>(cK + sk_off(i * 32 + col, 2 * t + hq));
+  f32x16 s;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t], qf[t], s, 0, 0, 0);
+  return s;
+}
+
+// P = exp2(S s log2e - c2) for one half, added to the lane's row sum and packed (bf16) as the two
+// 16-key B operands of O^T += V^T P^T. Accumulator register r of lane l holds key
+// 8 (r >> 2) + 4 (l >> 5) + (r & 3) of the half. kMask: keys at half positions >= `valid` get P = 0.
+template <bool kMask>
+__device__ __forceinline__ void softmax_half(const f32x16& s, float scale_log2, float c2, int hq, int valid,
+                                             float& lsum, bf16x8 (&pf)[2]) {
+#pragma clang fp contract(off)
+  float p[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, -c2));
+    if constexpr (kMask) x = (r >> 2) * 8 + hq * 4 + (r & 3) < valid ? x : 0.0f;
+    p[r] = x;
+    lsum = lsum + x;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(p[8 * u + 2 * j], p[8 * u + 2 * j + 1]);
+    pf[u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+  }
+}
+
+// O^T += V^T P^T for one 32-key half (16-key groups 2 i, 2 i + 1 of the LDS tile): 8 MFMAs in four
+// independent accumulator chains.
+__device__ __forceinline__ void pv_half(const uint8_t* cV, int i, const bf16x8 (&pf)[2], f32x16 (&acc_o)[4], int col,
+                                        int hq) {
+  bf16x8 vf[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      vf[u][dt] = *reinterpret_cast<const bf16x8*>(cV + sv_off(dt * 32 + col, 2 * (2 * i + u) + hq));
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[u][dt], pf[u], acc_o[dt], 0, 0, 0);
+}
+
+// One step of the per-wave software pipeline over 32-key halves: the QK^T MFMAs of half h (K from
+// cK, half i_cur) are independent of the softmax of half h-1 (s_prev), so the two streams interleave
+// on the matrix and vector pipes; then half h-1's P V MFMAs (V from cV, half i_prev).
+template <bool kMask>
+__device__ __forceinline__ void pipeline_step(const uint8_t* cK, int i_cur, const uint8_t* cV, int i_prev,
+                                              const bf16x8 (&qf)[8], f32x16& s_prev, f32x16 (&acc_o)[4],
+                                              float& lsum, float scale_log2, float c2, int col, int hq,
+                                              int valid_prev) {
+  const f32x16 s_cur = qk_half(cK, i_cur, qf, col, hq);
+  bf16x8 pf[2];
+  softmax_half<kMask>(s_prev, scale_log2, c2, hq, valid_prev, lsum, pf);
+  pv_half(cV, i_prev, pf, acc_o, col, hq);
+  s_prev = s_cur;
+}
 
 // kShortKV: a separate instantiation for short key sequences (cross-attention over text tokens) so
 // the two uses can be specialized and profiled apart.
 template <bool kShortKV>
-__global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) uint8_t sK[BKV * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t sV[128 * BKV * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sK[kStages][kTileK];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[kStages][kTileV];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -71,6 +146,38 @@ __global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a)
   const int64_t q0 = (int64_t)blockIdx.x * BQ + wave * 32;
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int hq = lane >> 5;
+
+  // K rows >= Sk fall outside the resource's extent and read as zero; V^T is padded to vt_ld.
+  const u32x4 r_k = buffer_rsrc(a.k + h * a.k_hs, (uint32_t)(((a.Sk - 1) * a.k_ss + 128) * 2));
+  const u32x4 r_v = buffer_rsrc(a.vt + (int64_t)h * 128 * a.vt_ld, (uint32_t)(128 * a.vt_ld * 2));
+  // DMA lane mapping: each wave fills 8 K rows (4 per 1 KiB instruction) and 16 V^T rows (8 per
+  // instruction); lane l lands in physical chunk l & 15 (K) / l & 7 (V) of its row and fetches the
+  // logical chunk the XOR swizzle assigns to that slot. The loads are issued through inline asm
+  // (invisible to the compiler's wait-count pass, which would otherwise wait for the prefetches
+  // before every LDS read); the loop waits for them itself.
+  const int k_row = lane >> 4, k_pc = lane & 15;
+  const int v_row = lane >> 3, v_pc = lane & 7;
+  auto issue_tile = [&](int kt) {
+    const int b = kt % kStages;
+    const int64_t kbase = (int64_t)kt * BKV;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = wave * 8 + i * 4 + k_row;
+      const int c = k_pc ^ (key & 15);
+      lds_dma_b128(r_k, (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int d = wave * 16 + i * 8 + v_row;
+      const int c = v_pc ^ (d & 7);
+      lds_dma_b128(r_v, (uint32_t)((d * a.vt_ld + kbase + c * 8) * 2), lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
+    }
+  };
+  const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
+  // The first three tiles go out before anything else, so their latency overlaps the Q loads.
+  issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  if (ntiles > 2) issue_tile(2);
 
   // ---- Q fragments (B operand): lane holds d = 16t + 8hq .. +7 of query q0 + col, t = 0..7 ----
   const __amdgpu_buffer_rsrc_t r_q =
@@ -91,9 +198,7 @@ __global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a)
   qn2 = qn2 + __shfl_xor(qn2, 32, 64);
   // c_i in log2 units: s * ||q_i|| * max||k|| * log2(e)
   const float c2 = a.scale_log2 * sqrtf(qn2) * a.kmax[h];
-
-  const __amdgpu_buffer_rsrc_t r_k = attn_rsrc(a.k + h * a.k_hs, ((a.Sk - 1) * a.k_ss + 128) * 2);
-  const __amdgpu_buffer_rsrc_t r_v = attn_rsrc(a.vt + (int64_t)h * 128 * a.vt_ld, 128 * a.vt_ld * 2);
+  const float sl2 = a.scale_log2;
 
   f32x16 acc_o[4];
 #pragma unroll
@@ -102,85 +207,40 @@ __global__ __launch_bounds__(256, 2) void attention_const_max_kernel(AttnArgs a)
     for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.0f;
   float lsum = 0.0f;
 
-  // DMA lane mapping: K rows 16 per wave (4 per 1 KiB instruction), V rows 32 per wave (8 per KiB)
-  const int k_row = lane >> 4, k_pc = lane & 15;
-  const int v_row = lane >> 3, v_pc = lane & 7;
-
-  const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const int64_t kbase = (int64_t)kt * BKV;
-    __syncthreads();  // every wave is done reading the previous tile
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = wave * 16 + i * 4 + k_row;
-      const int c = k_pc ^ (key & 15);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r_k, (__attribute__((address_space(3))) void*)(sK + (wave * 16 + i * 4) * 256), 16,
-          (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = wave * 32 + i * 8 + v_row;
-      const int c = v_pc ^ (d & 7);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r_v, (__attribute__((address_space(3))) void*)(sV + (wave * 32 + i * 8) * 128), 16,
-          (uint32_t)((d * a.vt_ld + kbase + c * 8) * 2), 0, 0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
+  // Pipeline over 32-key halves h = 2t + i: step h computes S(h) and the softmax and P V of h-1.
+  // Tile t is read by steps 2t .. 2t+2, so when every wave has passed the barrier at the top of tile
+  // t, tile t-2's slot is free and tile t+2 is loaded into it (two tiles of prefetch, one barrier per
+  // tile). The Q loads were issued after tiles 0-2, so the compiler's waits for them also cover
+  // tile 0; the explicit waits below cover the rest.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  __syncthreads();
+  f32x16 s_prev = qk_half(sK[0], 0, qf, col, hq);
+  const int sk_rem = (int)(a.Sk - (int64_t)(ntiles - 1) * BKV);  // keys in the last tile (1..64)
+  if (ntiles == 1)
+    pipeline_step<true>(sK[0], 1, sV[0], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, sk_rem);
+  else
+    pipeline_step<false>(sK[0], 1, sV[0], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
+  for (int t = 1; t < ntiles - 1; ++t) {
+    // outstanding: tiles t and t+1 (four loads each); wait for tile t
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
     __syncthreads();
-
-    // ---- S^T = K Q^T for two 32-key sub-tiles ----
-    f32x16 s[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
-      const int key = i * 32 + col;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sK + sk_off(key, 2 * t + hq));
-        s[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[i], 0, 0, 0);
-      }
-    }
-
-    // ---- P = exp2(S * s log2e - c2); lane-local row sums; pack P^T as bf16 B operands ----
-    const bool tail = kbase + BKV > a.Sk;
-    bf16x8 pf[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i][r], a.scale_log2, -c2));
-        if (tail) {
-          const int64_t key = kbase + i * 32 + (r >> 2) * 8 + hq * 4 + (r & 3);
-          x = key < a.Sk ? x : 0.0f;
-        }
-        p[r] = x;
-        lsum = lsum + x;
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(p[8 * u + 2 * j], p[8 * u + 2 * j + 1]);
-        pf[i][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
-      }
-    }
-
-    // ---- O^T += V^T P^T ----
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int d = dt * 32 + col;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int g = i * 2 + u;  // 16-key group within the tile
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(sV + sv_off(d, 2 * g + hq));
-          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[i][u], acc_o[dt], 0, 0, 0);
-        }
-    }
+    if (t + 2 < ntiles) issue_tile(t + 2);
+    const uint8_t* kc = sK[t % kStages];
+    pipeline_step<false>(kc, 0, sV[(t - 1) % kStages], 1, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
+    pipeline_step<false>(kc, 1, sV[t % kStages], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
+  }
+  if (ntiles > 1) {
+    const int t = ntiles - 1;
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    const uint8_t* kc = sK[t % kStages];
+    pipeline_step<false>(kc, 0, sV[(t - 1) % kStages], 1, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
+    pipeline_step<true>(kc, 1, sV[t % kStages], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, sk_rem);
+  }
+  {  // drain: softmax and P V of the last half
+    bf16x8 pf[2];
+    softmax_half<true>(s_prev, sl2, c2, hq, sk_rem - 32, lsum, pf);
+    pv_half(sV[(ntiles - 1) % kStages], 1, pf, acc_o, col, hq);
   }
 
   // ---- normalize and store ----
@@ -339,8 +399,8 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   a.os_ss = os_token_stride;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
   if (Sk <= 1024)
-    hipLaunchKernelGGL(attention_const_max_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(attention_const_max_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(attention_const_max_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(attention_const_max_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   return check_launch("wanmi_attention_const_max");
 }
