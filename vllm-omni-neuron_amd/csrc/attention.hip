@@ -62,31 +62,31 @@ constexpr int kTileK = BKV * 256;      // bytes of one K tile
 constexpr int kTileV = 128 * BKV * 2;  // bytes of one V^T tile
 constexpr int kLoadsPerTile = 4;       // direct-to-LDS instructions per wave per tile (2 K + 2 V)
 
-// S^T of one 32-key half (keys 32 i .. 32 i + 31 of the LDS tile) against the wave's 32 queries:
-// 8 MFMAs over d, K fragments read ahead of the chain.
-__device__ __forceinline__ f32x16 qk_half(const uint8_t* cK, int i, const bf16x8 (&qf)[8], int col, int hq) {
+// Logits of one 32-key half (keys 32 i .. 32 i + 31 of the LDS tile) against the wave's 32 queries,
+// in log2 units and already shifted by the bound: S^T = -c2 + K (s log2e Q)^T. The chain starts from
+// `negc` (every register -c2 of the lane's query), so the softmax needs no per-element scale or
+// subtraction. 8 MFMAs over d, K fragments read ahead of the chain.
+__device__ __forceinline__ f32x16 qk_half(const uint8_t* cK, int i, const bf16x8 (&qf)[8], const f32x16& negc,
+                                          int col, int hq) {
   bf16x8 kf[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) kf[t] = *reinterpret_cast<const bf16x8*>(cK + sk_off(i * 32 + col, 2 * t + hq));
-  f32x16 s;
+  f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], negc, 0, 0, 0);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t], qf[t], s, 0, 0, 0);
+  for (int t = 1; t < 8; ++t) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t], qf[t], s, 0, 0, 0);
   return s;
 }
 
-// P = exp2(S s log2e - c2) for one half, added to the lane's row sum and packed (bf16) as the two
-// 16-key B operands of O^T += V^T P^T. Accumulator register r of lane l holds key
+// P = exp2(S) for one half of shifted log2 logits, added to the lane's row sum and packed (bf16) as
+// the two 16-key B operands of O^T += V^T P^T. Accumulator register r of lane l holds key
 // 8 (r >> 2) + 4 (l >> 5) + (r & 3) of the half. kMask: keys at half positions >= `valid` get P = 0.
 template <bool kMask>
-__device__ __forceinline__ void softmax_half(const f32x16& s, float scale_log2, float c2, int hq, int valid,
-                                             float& lsum, bf16x8 (&pf)[2]) {
+__device__ __forceinline__ void softmax_half(const f32x16& s, int hq, int valid, float& lsum, bf16x8 (&pf)[2]) {
 #pragma clang fp contract(off)
   float p[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], scale_log2, -c2));
+    float x = __builtin_amdgcn_exp2f(s[r]);
     if constexpr (kMask) x = (r >> 2) * 8 + hq * 4 + (r & 3) < valid ? x : 0.0f;
     p[r] = x;
     lsum = lsum + x;
@@ -121,12 +121,11 @@ __device__ __forceinline__ void pv_half(const uint8_t* cV, int i, const bf16x8 (
 // on the matrix and vector pipes; then half h-1's P V MFMAs (V from cV, half i_prev).
 template <bool kMask>
 __device__ __forceinline__ void pipeline_step(const uint8_t* cK, int i_cur, const uint8_t* cV, int i_prev,
-                                              const bf16x8 (&qf)[8], f32x16& s_prev, f32x16 (&acc_o)[4],
-                                              float& lsum, float scale_log2, float c2, int col, int hq,
-                                              int valid_prev) {
-  const f32x16 s_cur = qk_half(cK, i_cur, qf, col, hq);
+                                              const bf16x8 (&qf)[8], const f32x16& negc, f32x16& s_prev,
+                                              f32x16 (&acc_o)[4], float& lsum, int col, int hq, int valid_prev) {
+  const f32x16 s_cur = qk_half(cK, i_cur, qf, negc, col, hq);
   bf16x8 pf[2];
-  softmax_half<kMask>(s_prev, scale_log2, c2, hq, valid_prev, lsum, pf);
+  softmax_half<kMask>(s_prev, hq, valid_prev, lsum, pf);
   pv_half(cV, i_prev, pf, acc_o, col, hq);
   s_prev = s_cur;
 }
@@ -193,12 +192,19 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
       qn2 = qn2 + lo * lo;
       qn2 = qn2 + hi * hi;
     }
-    qf[t] = __builtin_bit_cast(bf16x8, v);
+    // the MFMA operand is Q pre-scaled by s log2(e) and rounded to bf16 (the reference pre-scales Q
+    // by s before its QK^T as well), so the logits come out in log2 units
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(bf16_lo(v[j]) * a.scale_log2, bf16_hi(v[j]) * a.scale_log2);
+    qf[t] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
   }
   qn2 = qn2 + __shfl_xor(qn2, 32, 64);
-  // c_i in log2 units: s * ||q_i|| * max||k|| * log2(e)
+  // c_i in log2 units: s * ||q_i|| * max||k|| * log2(e), from the unscaled bf16 Q
   const float c2 = a.scale_log2 * sqrtf(qn2) * a.kmax[h];
-  const float sl2 = a.scale_log2;
+  f32x16 negc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negc[r] = -c2;
 
   f32x16 acc_o[4];
 #pragma unroll
@@ -214,32 +220,35 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   // tile 0; the explicit waits below cover the rest.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
-  f32x16 s_prev = qk_half(sK[0], 0, qf, col, hq);
+  f32x16 s_prev = qk_half(sK[0], 0, qf, negc, col, hq);
   const int sk_rem = (int)(a.Sk - (int64_t)(ntiles - 1) * BKV);  // keys in the last tile (1..64)
   if (ntiles == 1)
-    pipeline_step<true>(sK[0], 1, sV[0], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, sk_rem);
+    pipeline_step<true>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
   else
-    pipeline_step<false>(sK[0], 1, sV[0], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
-  for (int t = 1; t < ntiles - 1; ++t) {
-    // outstanding: tiles t and t+1 (four loads each); wait for tile t
+    pipeline_step<false>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+  // Tile t of the steady state (1 <= t < ntiles - 1): outstanding loads are tiles t and t+1 (four
+  // per wave each); wait for tile t, publish it, refill tile t-2's slot with tile t+2, then the two
+  // pipeline steps of t (`slot` = t % kStages).
+  auto steady_tile = [&](int t, int slot) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
     __syncthreads();
     if (t + 2 < ntiles) issue_tile(t + 2);
-    const uint8_t* kc = sK[t % kStages];
-    pipeline_step<false>(kc, 0, sV[(t - 1) % kStages], 1, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
-    pipeline_step<false>(kc, 1, sV[t % kStages], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
-  }
+    const int prev = (slot + kStages - 1) % kStages;
+    pipeline_step<false>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<false>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+  };
+  for (int t = 1; t < ntiles - 1; ++t) steady_tile(t, t % kStages);
   if (ntiles > 1) {
-    const int t = ntiles - 1;
+    const int tl = ntiles - 1;
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
-    const uint8_t* kc = sK[t % kStages];
-    pipeline_step<false>(kc, 0, sV[(t - 1) % kStages], 1, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, 32);
-    pipeline_step<true>(kc, 1, sV[t % kStages], 0, qf, s_prev, acc_o, lsum, sl2, c2, col, hq, sk_rem);
+    const uint8_t* kc = sK[tl % kStages];
+    pipeline_step<false>(kc, 0, sV[(tl - 1) % kStages], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<true>(kc, 1, sV[tl % kStages], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
   }
   {  // drain: softmax and P V of the last half
     bf16x8 pf[2];
-    softmax_half<true>(s_prev, sl2, c2, hq, sk_rem - 32, lsum, pf);
+    softmax_half<true>(s_prev, hq, sk_rem - 32, lsum, pf);
     pv_half(sV[(ntiles - 1) % kStages], 1, pf, acc_o, col, hq);
   }
 
