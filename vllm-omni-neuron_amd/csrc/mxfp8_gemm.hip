@@ -80,7 +80,12 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
+// LDS byte offset of 16-byte chunk `chunk` of operand row `row`. The chunk index is XORed with
+// f(row) = (row & 7) ^ ((row >> 3) & 1): the 16 lanes that one LDS cycle serves read rows r..r+15
+// (64 banks of 4 bytes = two 128-byte rows), and f gives the eight even rows, and the eight odd
+// rows, eight distinct chunk slots, so the MFMA operand reads are free of bank conflicts.
+__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ swz_f(row)) << 4); }
 
 // MFMA operands of one 64-deep k slice of a wave's 128 x 128 block: 4 weight-row and 4 token-row
 // fragments (32 bytes per lane each) and their e8m0 scale bytes.
@@ -165,50 +170,50 @@ __device__ __forceinline__ TileLoads tile_loads(const GemmArgs& g, int v) {
   return t;
 }
 
-// Codes of stage kt -> LDS stage buffer `buf`. Wave w fills rows 64w .. 64w+63 of each operand
-// tile, 8 rows (1 KiB) per instruction: lane l lands in physical 16-byte slot l & 7 of row
-// 8i + (l >> 3) and fetches the logical chunk the XOR swizzle assigns to that slot. One asm block
-// steps M0 (the LDS destination) and two VGPR offsets itself (every M0 write is followed by
-// another instruction before the load that reads it); the scalar offset stays 0.
-#define WANMI_DMA_ROW_PAIR                                   \
-  "buffer_load_dwordx4 %[tw], %[rw], 0 offen lds\n\t"        \
-  "s_add_u32 m0, m0, 0x8000\n\t"                             \
-  "v_add_u32 %[tw], %[wstep], %[tw]\n\t"                     \
-  "buffer_load_dwordx4 %[ta], %[ra], 0 offen lds\n\t"        \
-  "s_add_u32 m0, m0, 0xffff8400\n\t"                         \
-  "v_add_u32 %[ta], %[astep], %[ta]\n\t"
-static_assert(TN * BK == 0x8000 && 8 * BK - TN * BK == -0x7c00,
-              "M0 steps in the stage DMA assume 32 KiB operand tiles and 1 KiB row groups");
-
 // !valid: an empty extent turns every load into a zero fill that moves no memory (branch-free)
 __device__ __forceinline__ u32x4 maybe_empty(u32x4 r, bool valid) {
   r[2] = valid ? r[2] : 0u;
   return r;
 }
 
-__device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
-                                            uint32_t voff_w, uint32_t voff_a, bool valid = true) {
-  const u32x4 rw = maybe_empty(t.w, valid), ra = maybe_empty(t.a, valid);
-  const uint32_t k0 = (uint32_t)kt * BK;
-  const uint32_t vw = voff_w + (uint32_t)(wave * 64 * g.K) + k0;
-  const uint32_t va = voff_a + (uint32_t)(wave * 64 * g.lda) + k0;
-  const uint32_t wstep = (uint32_t)(8 * g.K), astep = (uint32_t)(8 * g.lda);
-  const uint32_t lw = lds_addr(buf) + wave * 64 * BK;
-  uint32_t tw, ta;
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile(
-      "s_mov_b32 m0, %[lw]\n\t"
-      "v_mov_b32 %[tw], %[vw]\n\t"
-      "v_mov_b32 %[ta], %[va]\n\t"
-      WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR
-      WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR WANMI_DMA_ROW_PAIR
-      : [tw] "=&v"(tw), [ta] "=&v"(ta)
-      : [vw] "v"(vw), [va] "v"(va), [rw] "s"(rw), [ra] "s"(ra), [wstep] "s"(wstep), [astep] "s"(astep), [lw] "s"(lw)
-      : "memory", "m0", "scc");
-#pragma clang diagnostic pop
+// Direct-to-LDS loads of the codes of one stage into an LDS stage buffer. Wave w fills rows
+// 64w .. 64w+63 of each operand tile, 8 rows (1 KiB) per instruction: in row group p (rows
+// 64w + 8p + (l >> 3)) lane l lands in physical 16-byte slot l & 7 and fetches the logical chunk
+// (l & 7) ^ f(row) = (l & 7) ^ (l >> 3) ^ (p & 1). The loads go in pairs (row group p of W and of
+// the activations) so they can be spread between MFMAs; lane offsets are recomputed per pair from
+// the lane id (a few VALU ops, which this kernel has to spare) rather than held in registers.
+__device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
+                                              int p, bool valid = true) {
+  const int l = fresh_lane_id();
+  const int srow = l >> 3;
+  const uint32_t col = (uint32_t)kt * BK + (uint32_t)((((l & 7) ^ srow ^ (p & 1))) << 4);
+  const uint32_t row = (uint32_t)(wave * 64 + p * 8 + srow);
+  const uint32_t lds = lds_addr(buf) + (uint32_t)(wave * 64 + p * 8) * BK;
+  lds_dma_b128(maybe_empty(t.w, valid), row * (uint32_t)g.K + col, lds);
+  lds_dma_b128(maybe_empty(t.a, valid), row * (uint32_t)g.lda + col, lds + TN * BK);
 }
-#undef WANMI_DMA_ROW_PAIR
+
+__device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
+                                            bool valid = true) {
+#pragma unroll
+  for (int p = 0; p < 8; ++p) code_dma_pair(g, t, kt, buf, wave, p, valid);
+}
+
+// The MFMAs of weight-row fragments 0 and 1 (8 of them) with the 16 code loads of a stage spread
+// between them, two after each MFMA. Issued as one block, the loads would hold the wave at the
+// texture unit's input queue (each moves 1 KiB) while its matrix pipe runs dry; spread out, each
+// pair issues while an MFMA executes. The scheduling barriers keep the compiler from regrouping them.
+__device__ __forceinline__ void mfma_rows01_with_dma(const SliceOperands& op, f32x16 (&acc)[4][4], const GemmArgs& g,
+                                                     const TileLoads& t, int kt, uint8_t* buf, int wave, bool valid) {
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int i = p >> 2, j = p & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
+                                                                 op.as[j]);
+    code_dma_pair(g, t, kt, buf, wave, p, valid);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
 
 // Scale bytes of stage group grp (stages 4 grp .. 4 grp + 3, k-blocks [16 grp, 16 grp + 16)) ->
 // `sc` ([2][256] x 16 B). Lane l of wave w copies the 16 bytes of row 64w + l of each operand.
@@ -377,11 +382,6 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
   const int r32 = lane & 31;
   const int KT = (int)(g.K / BK);
   const int total = g.tiles_m * g.tiles_n;
-  // lane parts of the DMA offsets (the same for every tile and stage)
-  const int srow = lane >> 3;
-  const int schunk = (lane & 7) ^ (srow & 7);
-  const uint32_t voff_w = (uint32_t)(srow * g.K + schunk * 16);
-  const uint32_t voff_a = (uint32_t)(srow * g.lda + schunk * 16);
   // Prefetching the next tile before the epilogue would make the gated-residual epilogue's own
   // residual loads wait behind those loads (the wait counter is in order), so that epilogue
   // prefetches after.
@@ -390,8 +390,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
   auto prefetch = [&](const TileLoads& tl, float* vec) {
     issue_vectors(g, tl, vec, wave);
     issue_scales(g, tl, 0, ssc[0], wave);
-    issue_codes(g, tl, 0, smem0, wave, voff_w, voff_a);
-    if constexpr (kPipelined) issue_codes(g, tl, 1, smem1, wave, voff_w, voff_a);
+    issue_codes(g, tl, 0, smem0, wave);
+    if constexpr (kPipelined) issue_codes(g, tl, 1, smem1, wave);
   };
 
   int v = blockIdx.x;
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
         // nobody reads nxt, nor the other scale buffer, since the last barrier
         if (kt + 1 < KT) {
           if ((kt + 1) % kScaleGroup == 0) issue_scales(g, t, (kt + 1) / kScaleGroup, ssc[((kt + 1) / kScaleGroup) & 1], wave);
-          issue_codes(g, t, kt + 1, nxt, wave, voff_w, voff_a);
+          issue_codes(g, t, kt + 1, nxt, wave);
         }
         SliceOperands op;
         read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32);
@@ -434,7 +434,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
       // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], word
       // s % 4. Per stage: the slice-0 MFMAs run while slice 1 is read; a barrier (every wave has
       // read the stage) lets the loads of stage s+2 go into the same buffer during the first half
-      // of the slice-1 MFMAs; a second barrier (every wave's stage s+1 has landed) lets slice 0 of
+      // of the slice-1 MFMAs (spread between them: mfma_rows01_with_dma); a second barrier (every
+      // wave's stage s+1 has landed) lets slice 0 of
       // stage s+1 be read during the second half. The scales of group g+1 are loaded with stage
       // 4g+4's codes. The body has no branches (conditional issue makes the register allocator
       // spill operands): in the last iteration the loads past the end are issued against an empty
@@ -448,8 +449,7 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     __syncthreads(); /* every wave has read CUR */                                                 \
     const bool more_ = (S) + 2 < KT;                                                               \
     if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
-    issue_codes(g, t, more_ ? (S) + 2 : 0, CUR, wave, voff_w, voff_a, more_);                      \
-    mfma_rows<0, 2>(opB, acc);                                                                     \
+    mfma_rows01_with_dma(opB, acc, g, t, more_ ? (S) + 2 : 0, CUR, wave, more_);                   \
     /* stage S+1 landed: only stage S+2's loads may still be in flight */                         \
     __builtin_amdgcn_s_waitcnt(waitcnt_vm((WITH_SCALES) ? kCodeLoads + kScaleLoads : kCodeLoads));  \
     __syncthreads();                                                                               \
