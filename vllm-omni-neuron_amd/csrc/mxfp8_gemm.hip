@@ -251,17 +251,35 @@ __device__ __forceinline__ void init_vectors(const GemmArgs& g, float (*svec)[kV
   }
 }
 
-// One 32 x 32 accumulator tile: lane holds token m and n = nt + 8*gi + 4*h + q (gi, q in 0..3);
-// nt, mt are the tile's offsets inside the workgroup tile (vector indices in LDS).
-template <int EPI>
-__device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a, const float* vec, int m,
-                                              int n0, int nt, int mt, int h, const uint2* res) {
+// ------------------------------------------------------------------------------------------------
+// Epilogue. The accumulator of tile (i, j) gives lane l token 32 j + (l & 31) of the wave's block and
+// features n = 32 i + 8 g + 4 (l >> 5) + q (g, q in 0..3), so the per-element math (scales, bias,
+// GELU, bf16 rounding, MX block exponent with one exchange with lane l ^ 32) is lane-local. Stored
+// straight from that layout, one store instruction would touch 32 rows; instead each wave stages
+// 64 tokens at a time in its own 16 KiB of LDS and stores whole row segments: 16 lanes x 16 bytes
+// = one token's 256-byte bf16 segment (8 lanes for the 128-byte e4m3 segment), 8 full cache lines
+// per instruction, half as many instructions.
+// ------------------------------------------------------------------------------------------------
+constexpr int kStageWave = 16384;  // LDS staging bytes per wave
+
+// Output stores are non-temporal: the tile is written once and read by the next kernel long after it
+// would have left L2, and streaming it past L2 keeps the stores from competing with the operand
+// traffic of the tiles still in their main loops (measured: 0.2 ms of 2.7 on the QKV projection).
+__device__ __forceinline__ void store_nt16(void* p, uint4 d) {
+  __builtin_nontemporal_store(u32x4{d.x, d.y, d.z, d.w}, reinterpret_cast<u32x4*>(p));
+}
+
+// bf16 staging: [64 tokens][256 B], 16-byte chunk index XOR (token & 15) -- the 16 lanes of an LDS
+// cycle hit 16 distinct chunks both when writing (16 tokens, one chunk) and reading (one token).
+__device__ __forceinline__ int stg16(int tok, int chunk) { return tok * 256 + ((chunk ^ (tok & 15)) << 4); }
+// e4m3 staging: [64 tokens][128 B], chunk XOR ((token >> 1) & 7) (two 128-byte rows per bank cycle).
+__device__ __forceinline__ int stg8(int tok, int chunk) { return tok * 128 + ((chunk ^ ((tok >> 1) & 7)) << 4); }
+
+// Scaled, biased accumulator values of tile (i, j) for this lane: v = (acc * row_scale) * col_scale
+// + bias (absent vectors hold their neutral values, so this is exact without them).
+__device__ __forceinline__ void epi_values(const f32x16& a, const float* vec, int nt, int mt, int h, float (&v)[16]) {
 #pragma clang fp contract(off)
-  const bool mok = m < (int)g.M;
-  const uint32_t row = (uint32_t)m * (uint32_t)g.ldo;  // element offset of the lane's output row (< 2^32)
-  // absent vectors hold their neutral values (bias -0, scales 1), so this is exact without them
   const float rsc = vec[768 + mt];
-  float v[16];
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi) {
     const int nl = nt + gi * 8 + h * 4;
@@ -272,94 +290,125 @@ __device__ __forceinline__ void epilogue_tile(const GemmArgs& g, const f32x16& a
 #pragma unroll
     for (int q = 0; q < 4; ++q) v[gi * 4 + q] = (a[gi * 4 + q] * rsc) * cc[q] + bb[q];
   }
-  if constexpr (EPI == WANMI_EPI_BF16 || EPI == WANMI_EPI_GELU_BF16) {
-    uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-      const uint32_t nb = (uint32_t)(n0 + nt + gi * 8 + h * 4);
-      float y[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) y[q] = EPI == WANMI_EPI_GELU_BF16 ? gelu_tanh(v[gi * 4 + q]) : v[gi * 4 + q];
-      if (mok)
-        *reinterpret_cast<uint2*>(out + (row + nb)) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
-    }
-  } else if constexpr (EPI == WANMI_EPI_GELU_MX) {
-    float y[16];
-    int e = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      y[q] = round_bf16(gelu_tanh(v[q]));
-      e = max(e, exp_field(y[q]));
-    }
-    e = max_with_lane_xor32(e);  // lanes l and l^32 hold the two halves of the 32-block
-    const int s = max(e - 7, 0);
-    const float f = mx_inv_scale(s);
-    uint8_t* codes = reinterpret_cast<uint8_t*>(g.out);
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-      const uint32_t nb = (uint32_t)(n0 + nt + gi * 8 + h * 4);
-      const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
-      if (mok) *reinterpret_cast<uint32_t*>(codes + (row + nb)) = c4;
-    }
-    if (mok && h == 0) g.out_scales[(uint32_t)m * (uint32_t)(g.N / 32) + (uint32_t)((n0 + nt) / 32)] = (uint8_t)s;
-  } else {  // gated residual: out = bf16(res + bf16(v) * gate)
-    uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-      const int nl = nt + gi * 8 + h * 4;
-      const uint2 r = res[gi];
-      const float4 gt = *reinterpret_cast<const float4*>(vec + 512 + nl);
-      const float rr[4] = {bf16_lo(r.x), bf16_hi(r.x), bf16_lo(r.y), bf16_hi(r.y)};
-      const float gg[4] = {gt.x, gt.y, gt.z, gt.w};
-      float y[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float f = round_bf16(v[gi * 4 + q]);
-        const float prod = f * gg[q];
-        y[q] = rr[q] + prod;
-      }
-      if (mok) *reinterpret_cast<uint2*>(out + (row + (uint32_t)(n0 + nl))) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
-    }
-  }
 }
 
+// One wave's 128 x 128 block: two halves of 64 tokens (accumulator columns j = 2 hf, 2 hf + 1).
+// `stage` is the wave's private LDS staging area; LDS operations of one wave complete in order, so
+// the read-back needs no barrier.
 template <int EPI>
-__device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec, int m0, int n0,
-                                         int wm, int wn, int lane) {
-  const int h = lane >> 5;
-  if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) {
-    // all 64 residual loads of the wave first (one latency), then the arithmetic
-    uint2 res[4][4][4];
+__device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec, uint8_t* stage,
+                                         int m0, int n0, int wm, int wn) {
+#pragma clang fp contract(off)
+  const int lane = fresh_lane_id();
+  const int h = lane >> 5, r32 = lane & 31;
+  const int nw = n0 + wn * 128;  // first feature of the wave's block
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + wm * 128 + j * 32 + (lane & 31);
-      const bool mok = m < (int)g.M;
-      const uint32_t row = (uint32_t)m * (uint32_t)g.ldo;
+  for (int hf = 0; hf < 2; ++hf) {
+    // ---- lane-local math, results into the staging area ----
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * hf + jj;
+      const int tok = jj * 32 + r32;  // token within the half
+      [[maybe_unused]] uint32_t sbytes = 0;
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const uint32_t nb = (uint32_t)(n0 + wn * 128 + i * 32 + gi * 8 + h * 4);
-          res[i][j][gi] = mok ? *reinterpret_cast<const uint2*>(g.residual + (row + nb)) : make_uint2(0, 0);
+      for (int i = 0; i < 4; ++i) {
+        float v[16];
+        epi_values(acc[i][j], vec, wn * 128 + i * 32, wm * 128 + j * 32 + r32, h, v);
+        if constexpr (EPI == WANMI_EPI_GELU_MX) {
+          float y[16];
+          int e = 0;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            y[q] = round_bf16(gelu_tanh(v[q]));
+            e = max(e, exp_field(y[q]));
+          }
+          e = max_with_lane_xor32(e);  // lanes l and l^32 hold the two halves of the 32-block
+          const int sx = max(e - 7, 0);
+          const float f = mx_inv_scale(sx);
+          sbytes |= (uint32_t)sx << (8 * i);
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            // features 32 i + 8 gi + 4 h .. +3: chunk 2 i + (gi >> 1), byte 8 (gi & 1) + 4 h
+            const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+            *reinterpret_cast<uint32_t*>(stage + stg8(tok, 2 * i + (gi >> 1)) + 8 * (gi & 1) + 4 * h) = c4;
+          }
+        } else {
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            float y[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float x = v[gi * 4 + q];
+              y[q] = EPI == WANMI_EPI_GELU_BF16 ? gelu_tanh(x) : x;  // gated residual: bf16(v) here
+            }
+            // features 32 i + 8 gi + 4 h .. +3: chunk 4 i + gi, byte 8 h
+            *reinterpret_cast<uint2*>(stage + stg16(tok, 4 * i + gi) + 8 * h) =
+                make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+          }
         }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        epilogue_tile<EPI>(g, acc[i][j], vec, m0 + wm * 128 + j * 32 + (lane & 31), n0, wn * 128 + i * 32,
-                           wm * 128 + j * 32 + (lane & 31), h, res[i][j]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        epilogue_tile<EPI>(g, acc[i][j], vec, m0 + wm * 128 + j * 32 + (lane & 31), n0, wn * 128 + i * 32,
-                           wm * 128 + j * 32 + (lane & 31), h, nullptr);
-        // one accumulator tile at a time: interleaving tiles raises register pressure into spills,
-        // and a spill reload would wait for the next tile's in-flight loads
-        __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (EPI == WANMI_EPI_GELU_MX) {
+        const int m = m0 + wm * 128 + j * 32 + r32;
+        if (h == 0 && m < (int)g.M)
+          __builtin_nontemporal_store(sbytes, reinterpret_cast<uint32_t*>(g.out_scales + (uint32_t)m * (uint32_t)(g.N / 32) +
+                                                                         (uint32_t)(nw / 32)));
+      }
+    }
+    // ---- read back whole row segments and store them ----
+    const int mbase = m0 + wm * 128 + hf * 64;
+    if constexpr (EPI == WANMI_EPI_GELU_MX) {
+      uint8_t* codes = reinterpret_cast<uint8_t*>(g.out);
+      const int chunk = lane & 7;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int tok = it * 8 + (lane >> 3);
+        const uint4 d = *reinterpret_cast<const uint4*>(stage + stg8(tok, chunk));
+        const int m = mbase + tok;
+        if (m < (int)g.M) store_nt16(codes + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 16)), d);
+      }
+    } else if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) {
+      // out = bf16(res + bf16(v) * gate), 8 features per lane; the residual is read coalesced too
+      uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
+      const int chunk = lane & 15;
+      uint4 res[16];
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int m = mbase + it * 4 + (lane >> 4);
+        res[it] = m < (int)g.M ? *reinterpret_cast<const uint4*>(g.residual + ((uint32_t)m * (uint32_t)g.ldo +
+                                                                            (uint32_t)(nw + chunk * 8)))
+                               : make_uint4(0, 0, 0, 0);
+      }
+      const float4 g0 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8);
+      const float4 g1 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8 + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int tok = it * 4 + (lane >> 4);
+        const uint4 d = *reinterpret_cast<const uint4*>(stage + stg16(tok, chunk));
+        const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+        const uint32_t rv[4] = {res[it].x, res[it].y, res[it].z, res[it].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float y0 = bf16_lo(rv[k]) + bf16_lo(dv[k]) * gg[2 * k];
+          const float y1 = bf16_hi(rv[k]) + bf16_hi(dv[k]) * gg[2 * k + 1];
+          o[k] = pack_bf16x2(y0, y1);
+        }
+        const int m = mbase + tok;
+        if (m < (int)g.M)
+          store_nt16(out + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 8)), make_uint4(o[0], o[1], o[2], o[3]));
+      }
+    } else {
+      uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
+      const int chunk = lane & 15;
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int tok = it * 4 + (lane >> 4);
+        const uint4 d = *reinterpret_cast<const uint4*>(stage + stg16(tok, chunk));
+        const int m = mbase + tok;
+        if (m < (int)g.M) store_nt16(out + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 8)), d);
+      }
+    }
   }
 }
 
@@ -386,24 +435,33 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
   // residual loads wait behind those loads (the wait counter is in order), so that epilogue
   // prefetches after.
   constexpr bool kPrefetchBeforeEpilogue = EPI != WANMI_EPI_GATED_RESIDUAL;
-
-  auto prefetch = [&](const TileLoads& tl, float* vec) {
+  // The epilogue stages its output in smem1, so only stage 0 of the next tile (smem0, with the
+  // first scale group and the epilogue vectors) may be loaded before or during it; stage 1 follows.
+  auto prefetch0 = [&](const TileLoads& tl, float* vec) {
     issue_vectors(g, tl, vec, wave);
     issue_scales(g, tl, 0, ssc[0], wave);
     issue_codes(g, tl, 0, smem0, wave);
+  };
+  auto prefetch1 = [&](const TileLoads& tl) {
     if constexpr (kPipelined) issue_codes(g, tl, 1, smem1, wave);
   };
 
   int v = blockIdx.x;
   init_vectors(g, svec, tid);  // published by the barrier at the top of the tile loop
-  prefetch(tile_loads(g, v), svec[0]);
+  prefetch0(tile_loads(g, v), svec[0]);
+  prefetch1(tile_loads(g, v));
   int vb = 0;
 
   f32x16 acc[4][4];
   for (;;) {
     // tile state is recomputed per tile (cheap scalar work) rather than carried across the epilogue
     const TileLoads t = tile_loads(g, v);
-    __builtin_amdgcn_s_waitcnt(0);  // this tile's first stages, scales and vectors have landed
+    // This tile's stage 0, scales and vectors have landed; in the pipelined loop stage 1 (the
+    // youngest 16 loads) may still be in flight.
+    if constexpr (kPipelined)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCodeLoads));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -469,21 +527,20 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #undef WANMI_GEMM_STAGE
     }
 
-    // Every wave is past its last LDS operand read of this tile (the last barrier above follows
-    // them), so the stage buffers may be refilled with the next tile.
+    // Every wave is past its last LDS operand read of this tile once all have passed a barrier, and
+    // the zero-fill loads past the end of K (which target the stage buffers) are complete after
+    // vmcnt(0); then smem0 may take the next tile's stage 0 and smem1 serves as staging.
     const int m0 = (int)t.m0, n0 = (int)t.n0;
     const int vn = v + (int)gridDim.x;
     const bool has_next = vn < total;
-    if (kPrefetchBeforeEpilogue && has_next) {
-      __syncthreads();
-      prefetch(tile_loads(g, vn), svec[vb ^ 1]);
-    }
-    epilogue<EPI>(g, acc, svec[vb], m0, n0, wm, wn, fresh_lane_id());
-    if (!kPrefetchBeforeEpilogue && has_next) {
-      __syncthreads();
-      prefetch(tile_loads(g, vn), svec[vb ^ 1]);
-    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    if (kPrefetchBeforeEpilogue && has_next) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
+    epilogue<EPI>(g, acc, svec[vb], smem1 + wave * kStageWave, m0, n0, wm, wn);
     if (!has_next) break;
+    __syncthreads();  // every wave is done with its staging area in smem1
+    if (!kPrefetchBeforeEpilogue) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
+    prefetch1(tile_loads(g, vn));
     v = vn;
     vb ^= 1;
   }
@@ -519,7 +576,7 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
                 "wanmi_mxfp8_gemm: unknown epilogue %d", epilogue);
   WANMI_REQUIRE(lda >= K && lda % 16 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: lda=%lld must be >= K and a multiple of 16",
                 (long long)lda);
-  WANMI_REQUIRE(ldo >= N && ldo % 4 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: ldo=%lld must be >= N and a multiple of 4",
+  WANMI_REQUIRE(ldo >= N && ldo % 16 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: ldo=%lld must be >= N and a multiple of 16",
                 (long long)ldo);
   if (M == 0) return WANMI_OK;
   WANMI_REQUIRE(a_codes && a_scales && w_codes && w_scales && out, WANMI_ERR_ARG,
@@ -530,9 +587,10 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
                 "wanmi_mxfp8_gemm: gated-residual epilogue needs residual and gate");
   WANMI_REQUIRE(((uintptr_t)a_codes % 16) == 0 && ((uintptr_t)w_codes % 16) == 0 &&
                     ((uintptr_t)a_scales % 4) == 0 && ((uintptr_t)w_scales % 4) == 0 &&
-                    ((uintptr_t)out % 8) == 0 && (!bias || ((uintptr_t)bias % 16) == 0) &&
+                    ((uintptr_t)out % 16) == 0 && (!out_scales || ((uintptr_t)out_scales % 4) == 0) &&
+                    (!bias || ((uintptr_t)bias % 16) == 0) &&
                     (!col_scale || ((uintptr_t)col_scale % 16) == 0) &&
-                    (!gate || ((uintptr_t)gate % 16) == 0) && (!residual || ((uintptr_t)residual % 8) == 0),
+                    (!gate || ((uintptr_t)gate % 16) == 0) && (!residual || ((uintptr_t)residual % 16) == 0),
                 WANMI_ERR_ARG, "wanmi_mxfp8_gemm: misaligned operand");
   const int64_t tiles = (N / TN) * ((M + TM - 1) / TM);
   WANMI_REQUIRE(tiles < (1LL << 31), WANMI_ERR_ARG, "wanmi_mxfp8_gemm: problem too large");
