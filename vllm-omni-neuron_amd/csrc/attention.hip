@@ -55,9 +55,12 @@ struct AttnArgs {
 
 // LDS tiles, a ring of kStages (tile t in slot t % kStages):
 //   sK: [64 keys][128 d] bf16, 16-byte chunk index XOR (key & 15)
-//   sV: [128 d][64 slots] bf16, 16-byte chunk index XOR (d & 7)
+//   sV: [128 d][64 slots] bf16, 16-byte chunk index XOR f(d) = (d & 7) ^ ((d >> 3) & 1)
+// One LDS cycle serves 16 lanes from 64 banks of 4 bytes: the K reads cover 16 keys (one 256-byte
+// row each, 16 distinct chunks); the V^T reads cover 16 d-rows of 128 bytes, two rows per bank
+// cycle, and f gives the eight even and the eight odd rows eight distinct chunks.
 __device__ __forceinline__ int sk_off(int key, int chunk) { return key * 256 + ((chunk ^ (key & 15)) << 4); }
-__device__ __forceinline__ int sv_off(int d, int chunk) { return d * 128 + ((chunk ^ (d & 7)) << 4); }
+__device__ __forceinline__ int sv_off(int d, int chunk) { return d * 128 + ((chunk ^ ((d & 7) ^ ((d >> 3) & 1))) << 4); }
 constexpr int kTileK = BKV * 256;      // bytes of one K tile
 constexpr int kTileV = 128 * BKV * 2;  // bytes of one V^T tile
 constexpr int kLoadsPerTile = 4;       // direct-to-LDS instructions per wave per tile (2 K + 2 V)
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int d = wave * 16 + i * 8 + v_row;
-      const int c = v_pc ^ (d & 7);
+      const int c = v_pc ^ (d & 7) ^ ((d >> 3) & 1);
       lds_dma_b128(r_v, (uint32_t)((d * a.vt_ld + kbase + c * 8) * 2), lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
     }
   };
