@@ -199,18 +199,18 @@ __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& 
   for (int p = 0; p < 8; ++p) code_dma_pair(g, t, kt, buf, wave, p, valid);
 }
 
-// The MFMAs of weight-row fragments 0 and 1 (8 of them) with the 16 code loads of a stage spread
-// between them, two after each MFMA. Issued as one block, the loads would hold the wave at the
-// texture unit's input queue (each moves 1 KiB) while its matrix pipe runs dry; spread out, each
-// pair issues while an MFMA executes. The scheduling barriers keep the compiler from regrouping them.
-__device__ __forceinline__ void mfma_rows01_with_dma(const SliceOperands& op, f32x16 (&acc)[4][4], const GemmArgs& g,
-                                                     const TileLoads& t, int kt, uint8_t* buf, int wave, bool valid) {
+// The 16 MFMAs of one slice with the 16 code loads of a stage spread between them, one pair after
+// every second MFMA. Issued as one block, the loads would hold the wave at the texture unit's input
+// queue (each moves 1 KiB) while its matrix pipe runs dry; spread out, each pair issues while an
+// MFMA executes. The scheduling barriers keep the compiler from regrouping them.
+__device__ __forceinline__ void mfma_all_with_dma(const SliceOperands& op, f32x16 (&acc)[4][4], const GemmArgs& g,
+                                                  const TileLoads& t, int kt, uint8_t* buf, int wave, bool valid) {
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int i = p >> 2, j = p & 3;
+  for (int q = 0; q < 16; ++q) {
+    const int i = q >> 2, j = q & 3;
     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
                                                                  op.as[j]);
-    code_dma_pair(g, t, kt, buf, wave, p, valid);
+    if (q & 1) code_dma_pair(g, t, kt, buf, wave, q >> 1, valid);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -490,24 +490,23 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
       }
     } else {
       // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], word
-      // s % 4. Per stage: the slice-0 MFMAs run while slice 1 is read; a barrier (every wave has
-      // read the stage) lets the loads of stage s+2 go into the same buffer during the first half
-      // of the slice-1 MFMAs (spread between them: mfma_rows01_with_dma); a second barrier (every
-      // wave's stage s+1 has landed) lets slice 0 of
-      // stage s+1 be read during the second half. The scales of group g+1 are loaded with stage
-      // 4g+4's codes. The body has no branches (conditional issue makes the register allocator
-      // spill operands): in the last iteration the loads past the end are issued against an empty
-      // resource, which moves no data and zero-fills buffers nobody reads again, and the slice
-      // read after the final barrier is dead.
+      // s % 4. Per stage: slice 1 is read and a barrier (every wave has read the stage) lets the
+      // loads of stage s+2 go into the same buffer, spread over the 16 slice-0 MFMAs, so they have
+      // one and a half stages to land; the first half of the slice-1 MFMAs follows; a second barrier
+      // (every wave's stage s+1 has landed) lets slice 0 of stage s+1 be read during the second half.
+      // The scales of group g+1 are loaded with stage 4g+4's codes. The body has no branches
+      // (conditional issue makes the register allocator spill operands): in the last iteration the
+      // loads past the end are issued against an empty resource, which moves no data and zero-fills
+      // buffers nobody reads again, and the slice read after the final barrier is dead.
 #define WANMI_GEMM_STAGE(S, CUR, OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                     \
   do {                                                                                             \
     read_slice(CUR, SC_CUR, Q_CUR, 1, opB, wn, wm, h, r32);                                        \
-    mfma_rows<0, 4>(opA, acc);                                                                     \
     __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                   \
     __syncthreads(); /* every wave has read CUR */                                                 \
     const bool more_ = (S) + 2 < KT;                                                               \
     if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
-    mfma_rows01_with_dma(opB, acc, g, t, more_ ? (S) + 2 : 0, CUR, wave, more_);                   \
+    mfma_all_with_dma(opA, acc, g, t, more_ ? (S) + 2 : 0, CUR, wave, more_);                      \
+    mfma_rows<0, 2>(opB, acc);                                                                     \
     /* stage S+1 landed: only stage S+2's loads may still be in flight */                         \
     __builtin_amdgcn_s_waitcnt(waitcnt_vm((WITH_SCALES) ? kCodeLoads + kScaleLoads : kCodeLoads));  \
     __syncthreads();                                                                               \
