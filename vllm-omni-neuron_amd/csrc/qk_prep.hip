@@ -36,6 +36,13 @@ struct QKNormArgs {
   float* maxnorm;  // [heads] or null (must be zeroed first)
 };
 
+// v with a DPP lane permutation applied (bound_ctrl: lanes without a source read 0; every control
+// used here has a source for every lane).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
 template <int NCH>
 __global__ __launch_bounds__(256, 2) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
 #pragma clang fp contract(off)
@@ -117,21 +124,35 @@ __global__ __launch_bounds__(256, 2) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
         }
         __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
         if (a.maxnorm) {
-          // one head = 16 consecutive lanes of a chunk
-          n2 = n2 + __shfl_xor(n2, 1, 64);
-          n2 = n2 + __shfl_xor(n2, 2, 64);
-          n2 = n2 + __shfl_xor(n2, 4, 64);
-          n2 = n2 + __shfl_xor(n2, 8, 64);
-          kmx[c] = fmaxf(kmx[c], sqrtf(n2));
+          // one head = 16 consecutive lanes of a chunk (one DPP row): sum over the row with DPP
+          // moves (quad xor 1, quad xor 2, half-row mirror, row mirror -- the pairs of an xor 1, 2,
+          // 4, 8 butterfly, no LDS round trips); the max is kept on ||k||^2 and square-rooted once
+          // at the end (sqrt is monotone and correctly rounded, so max(sqrt) = sqrt(max))
+          n2 = n2 + dpp_f32<0xB1>(n2);   // quad_perm(1,0,3,2)
+          n2 = n2 + dpp_f32<0x4E>(n2);   // quad_perm(2,3,0,1)
+          n2 = n2 + dpp_f32<0x141>(n2);  // row_half_mirror
+          n2 = n2 + dpp_f32<0x140>(n2);  // row_mirror
+          kmx[c] = fmaxf(kmx[c], n2);
         }
       }
     }
   }
-  if (a.maxnorm && (lane & 15) == 0) {
+  if (a.maxnorm) {
+    // Workgroup maximum first (through LDS), then one atomic per head per workgroup: every wave of
+    // the grid finishes at about the same time, and per-wave atomics on the same few cache lines
+    // serialize at the L2 (measured: 180 us of a 340 us launch).
+    __shared__ float smax[4][NCH * 4];
+    if ((lane & 15) == 0) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      if (c < a.nch)  // non-negative floats order like their bit patterns
-        atomicMax(reinterpret_cast<unsigned int*>(a.maxnorm) + c * 4 + (lane >> 4), __float_as_uint(kmx[c]));
+      for (int c = 0; c < NCH; ++c) smax[wave][c * 4 + (lane >> 4)] = kmx[c];
+    }
+    __syncthreads();
+    const int hd = threadIdx.x;
+    if (hd < a.heads) {
+      const float m = fmaxf(fmaxf(smax[0][hd], smax[1][hd]), fmaxf(smax[2][hd], smax[3][hd]));
+      // non-negative floats order like their bit patterns
+      atomicMax(reinterpret_cast<unsigned int*>(a.maxnorm) + hd, __float_as_uint(sqrtf(m)));
+    }
   }
 }
 
