@@ -276,9 +276,22 @@ __device__ __forceinline__ int stg16(int tok, int chunk) { return tok * 256 + ((
 __device__ __forceinline__ int stg8(int tok, int chunk) { return tok * 128 + ((chunk ^ ((tok >> 1) & 7)) << 4); }
 
 // Scaled, biased accumulator values of tile (i, j) for this lane: v = (acc * row_scale) * col_scale
-// + bias (absent vectors hold their neutral values, so this is exact without them).
-__device__ __forceinline__ void epi_values(const f32x16& a, const float* vec, int nt, int mt, int h, float (&v)[16]) {
+// + bias (absent vectors hold their neutral values, so this is exact without them). `scaled` is
+// false when neither scale vector is given (the MX-only projections): x * 1 == x exactly, so the two
+// multiplies and their LDS reads are skipped with the same result.
+__device__ __forceinline__ void epi_values(const f32x16& a, const float* vec, int nt, int mt, int h, bool scaled,
+                                           float (&v)[16]) {
 #pragma clang fp contract(off)
+  if (!scaled) {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const float4 b = *reinterpret_cast<const float4*>(vec + nt + gi * 8 + h * 4);
+      const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[gi * 4 + q] = a[gi * 4 + q] + bb[q];
+    }
+    return;
+  }
   const float rsc = vec[768 + mt];
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi) {
@@ -302,6 +315,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
   const int lane = fresh_lane_id();
   const int h = lane >> 5, r32 = lane & 31;
   const int nw = n0 + wn * 128;  // first feature of the wave's block
+  const bool scaled = g.row_scale || g.col_scale;
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     // ---- lane-local math, results into the staging area ----
@@ -313,7 +327,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v[16];
-        epi_values(acc[i][j], vec, wn * 128 + i * 32, wm * 128 + j * 32 + r32, h, v);
+        epi_values(acc[i][j], vec, wn * 128 + i * 32, wm * 128 + j * 32 + r32, h, scaled, v);
         if constexpr (EPI == WANMI_EPI_GELU_MX) {
           float y[16];
           int e = 0;
