@@ -45,18 +45,24 @@ def parse():
     return p.parse_args()
 
 
-def load_traffic():
+def load_traffic(seq_len):
     """HBM bytes per self-attention launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    (scaled by the same counters on a known-size copy); committed under profiles/."""
+    (scaled by the same counters on a known-size copy); committed under profiles/. None unless the
+    measurement was taken at this sequence length."""
     path = os.path.join(ROOT, "profiles", "self_attention_traffic.txt")
     if not os.path.exists(path):
         return None
+    vals = {}
     with open(path) as f:
         for line in f:
+            if line.lstrip().startswith("#"):
+                continue
             key, _, val = line.partition("=")
-            if key.strip() == "self_attention_bytes_per_launch":
-                return float(val)
-    return None
+            if val.strip():
+                vals[key.strip()] = float(val)
+    if vals.get("seq_len") != seq_len:
+        return None
+    return vals.get("self_attention_bytes_per_launch")
 
 
 class KernelTimer:
@@ -241,16 +247,16 @@ def main():
         "attn_tflops": round(attn_tflops, 1),
         "gemm_tflops": round(gemm_tflops, 1),
         "adaln_quant_gbs": round(adaln_gbs, 1),
-        "adaln_quant_us_32760x5120": round(first_adaln_us, 1),
+        "adaln_quant_plain_us": round(first_adaln_us, 1),
         "components": comp,
         "roofline": {
-            "kernel": "attention_const_max_kernel (self-attention, S=32760, 40 heads x 128)",
+            "kernel": f"attention_const_max_kernel (self-attention, S={S}, {HEADS} heads x {HEAD_DIM})",
             "bound": "mfma",
             "achieved": round(attn_tflops, 1),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": load_traffic(),
+            "traffic": load_traffic(S),
         },
     }
     if not args.no_cpu_baseline:

@@ -145,6 +145,31 @@ def test_self_attention_full_length_rows(pkg, dev):
         _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
 
 
+def test_self_attention_720p_rows(pkg, dev):
+    """Self-attention of the 720p step: 81 frames at 1280x720 = a 21x45x80 latent grid, 75600
+    tokens, 40 heads, normalized + RoPE'd q/k; 96 query rows over three heads (incl. the ragged last
+    query block) against exact fp64 attention over all 75600 keys."""
+    ops = pkg.attention_ops
+    grid = (21, 45, 80)
+    S, N = grid[0] * grid[1] * grid[2], 40
+    gdev = torch.Generator(device=dev).manual_seed(22)
+    qkv = torch.randn(S, 3 * N * 128, generator=gdev, device=dev).to(torch.bfloat16)
+    gamma = torch.ones(N * 128, device=dev)
+    cos, sin = orope.wan_rope(grid)
+    c64, s64 = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    ops.qk_rmsnorm_rope_(qkv[:, : N * 128], gamma, cos=c64, sin=s64)
+    kmax = ops.qk_rmsnorm_rope_(qkv[:, N * 128 : 2 * N * 128], gamma, cos=c64, sin=s64, want_max=True)
+    q = qkv[:, : N * 128].view(S, N, 128)
+    k = qkv[:, N * 128 : 2 * N * 128].view(S, N, 128)
+    v = qkv[:, 2 * N * 128 :].view(S, N, 128)
+    vt, _ = ops.transpose_heads(v)
+    out = ops.attention_core(q, k, vt, kmax, 128**-0.5)
+    rows = torch.tensor([0, 1, 255, 256, 37800, 75263, 75264, 75599] + list(range(50000, 50088)))[:96]
+    for h in (3, 20, 38):
+        ref = oa.torch_attend(q[rows, h].cpu(), k[:, h].cpu(), v[:, h].cpu(), 128**-0.5, dtype=torch.float64)
+        _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
+
+
 def test_dropins_match_reference_layouts(pkg, dev):
     ops = pkg.attention_ops
     B, N, S, D = 1, 4, 200, 128

@@ -131,3 +131,49 @@ def test_gemm_rejects_unsupported_shapes(pkg, dev):
     wq = pkg.quantize_weight_mx((torch.randn(256, 200, generator=g) * 0.02).to(torch.bfloat16).to(dev))
     with pytest.raises(NotImplementedError, match="multiple of 256"):
         pkg.mxfp8_linear(xq, wq)
+
+
+def test_gemm_full_mlp_shapes_row_subset(pkg, dev):
+    """MLP shapes of the GEMM workload: up [32760, 5120] x [5120, 13824] with the GELU-tanh epilogue
+    (bf16 and MX outputs) and down [32760, 13824] x [13824, 5120] with the gated-residual epilogue;
+    48 rows each (incl. the ragged last tile) against the fp64 oracle, MX codes bit-exact against
+    the MX quantization of the kernel's own bf16 GELU output."""
+    M, D, F = 32760, 5120, 13824
+    g = torch.Generator(device=dev).manual_seed(11)
+    rows = torch.tensor([0, 1, 255, 256, 4097, 16000, 32511, 32512] + list(range(32720, 32760)), device=dev)
+    # up + GELU
+    x = torch.randn(M, D, generator=g, device=dev).to(torch.bfloat16)
+    w_up = (torch.randn(D, F, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    b_up = torch.randn(F, generator=g, device=dev) * 0.1
+    xq = pkg.adaln_modulate(x, eps=0.0, norm_type="none", quant="mx")
+    wq = pkg.quantize_weight_mx(w_up, b_up)
+    y = pkg.mxfp8_linear(xq, wq, epilogue="gelu_bf16")[rows].cpu()
+    y_mx = pkg.mxfp8_linear(xq, wq, epilogue="gelu_mx")
+    ops = (
+        xq.codes.view(torch.uint8)[rows].cpu().numpy(), xq.scales[rows].cpu().numpy(),
+        wq.codes.view(torch.uint8).cpu().numpy(), wq.scales.cpu().numpy(),
+    )
+    _check(y, og.gelu_tanh(og.mx_gemm(*ops, bias=b_up.cpu().numpy())), og.abs_gemm(*ops) + 1e-3)
+    codes, scales = omx.mx_quantize(y.float().numpy())
+    np.testing.assert_array_equal(y_mx.scales[rows].cpu().numpy(), scales)
+    np.testing.assert_array_equal(y_mx.codes.view(torch.uint8)[rows].cpu().numpy(), codes)
+    del x, xq, w_up, wq, y_mx
+    # down + gated residual
+    h = torch.randn(M, F, generator=g, device=dev).to(torch.bfloat16)
+    w_dn = (torch.randn(F, D, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    b_dn = torch.randn(D, generator=g, device=dev) * 0.1
+    res = torch.randn(M, D, generator=g, device=dev).to(torch.bfloat16)
+    gate = torch.randn(D, generator=g, device=dev)
+    hq = pkg.adaln_modulate(h, eps=0.0, norm_type="none", quant="mx")
+    wq = pkg.quantize_weight_mx(w_dn, b_dn)
+    y = pkg.mxfp8_linear(hq, wq, epilogue="gated_residual", residual=res, gate=gate)[rows].cpu()
+    ops = (
+        hq.codes.view(torch.uint8)[rows].cpu().numpy(), hq.scales[rows].cpu().numpy(),
+        wq.codes.view(torch.uint8).cpu().numpy(), wq.scales.cpu().numpy(),
+    )
+    lin = og.mx_gemm(*ops, bias=b_dn.cpu().numpy())
+    gate_c = gate.cpu().double()
+    ref = res[rows].cpu().double() + lin.to(torch.bfloat16).double() * gate_c
+    err = (y.double() - ref).abs()
+    bound = 2.0**-8 * ref.abs() + (2.0**-7 * lin.abs() + 2.0**-14 * og.abs_gemm(*ops)) * gate_c.abs()
+    assert bool((err <= bound + 1e-30).all())

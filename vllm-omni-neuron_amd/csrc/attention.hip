@@ -135,7 +135,10 @@ __device__ __forceinline__ void pipeline_step(const uint8_t* cK, int i_cur, cons
 
 // kShortKV: a separate instantiation for short key sequences (cross-attention over text tokens) so
 // the two uses can be specialized and profiled apart.
-template <bool kShortKV>
+// kRebaseK: one head of K spans more than 2 GiB (the fused QKV layout, row stride 15360, at 720p), so
+// the K descriptor is rebuilt at each tile's first key; otherwise one descriptor covers the head and
+// the tile's offset travels in the wave-uniform soffset.
+template <bool kShortKV, bool kRebaseK>
 __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) uint8_t sK[kStages][kTileK];
@@ -149,8 +152,10 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int hq = lane >> 5;
 
-  // K rows >= Sk fall outside the resource's extent and read as zero; V^T is padded to vt_ld.
-  const u32x4 r_k = buffer_rsrc(a.k + h * a.k_hs, (uint32_t)(((a.Sk - 1) * a.k_ss + 128) * 2));
+  // Keys >= Sk fall outside the K descriptor's extent and read as zero. V^T ([128][vt_ld] per head,
+  // vt_ld >= Sk rounded up to 64) always fits one descriptor, and every tile lies inside it.
+  const uint16_t* k_head = a.k + h * a.k_hs;
+  const u32x4 r_k_head = buffer_rsrc(k_head, kRebaseK ? 0u : (uint32_t)(((a.Sk - 1) * a.k_ss + 128) * 2));
   const u32x4 r_v = buffer_rsrc(a.vt + (int64_t)h * 128 * a.vt_ld, (uint32_t)(128 * a.vt_ld * 2));
   // DMA lane mapping: each wave fills 8 K rows (4 per 1 KiB instruction) and 16 V^T rows (8 per
   // instruction); lane l lands in physical chunk l & 15 (K) / l & 7 (V) of its row and fetches the
@@ -162,17 +167,27 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   auto issue_tile = [&](int kt) {
     const int b = kt % kStages;
     const int64_t kbase = (int64_t)kt * BKV;
+    // The tile's key offset stays in the per-lane offset (soffset is not range-checked), so that
+    // keys >= Sk of the last tile read as zero.
+    u32x4 r_k = r_k_head;
+    int64_t key0 = kbase;
+    if constexpr (kRebaseK) {
+      const int64_t kvalid = a.Sk - kbase < BKV ? a.Sk - kbase : BKV;
+      r_k = buffer_rsrc(k_head + kbase * a.k_ss, (uint32_t)(((kvalid - 1) * a.k_ss + 128) * 2));
+      key0 = 0;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = wave * 8 + i * 4 + k_row;
       const int c = k_pc ^ (key & 15);
-      lds_dma_b128(r_k, (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+      lds_dma_b128(r_k, (uint32_t)(((key0 + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int d = wave * 16 + i * 8 + v_row;
       const int c = v_pc ^ (d & 7) ^ ((d >> 3) & 1);
-      lds_dma_b128(r_v, (uint32_t)((d * a.vt_ld + kbase + c * 8) * 2), lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
+      lds_dma_b128(r_v, (uint32_t)((d * a.vt_ld + c * 8) * 2), (uint32_t)(kbase * 2),
+                   lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
     }
   };
   const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
@@ -182,13 +197,15 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   if (ntiles > 2) issue_tile(2);
 
   // ---- Q fragments (B operand): lane holds d = 16t + 8hq .. +7 of query q0 + col, t = 0..7 ----
+  // Q through a descriptor based at the wave's first query; rows >= Sq read as zero.
+  const int64_t qvalid = a.Sq - q0 < 32 ? (a.Sq - q0 > 0 ? a.Sq - q0 : 0) : 32;
   const __amdgpu_buffer_rsrc_t r_q =
-      attn_rsrc(a.q + h * a.q_hs, ((a.Sq - 1) * a.q_ss + 128) * 2);  // rows >= Sq read as zero
+      attn_rsrc(a.q + h * a.q_hs + (qvalid > 0 ? q0 * a.q_ss : 0), qvalid > 0 ? ((qvalid - 1) * a.q_ss + 128) * 2 : 0);
   bf16x8 qf[8];
   float qn2 = 0.0f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)(((q0 + col) * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float lo = bf16_lo(v[j]), hi = bf16_hi(v[j]);
@@ -382,9 +399,10 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   WANMI_REQUIRE(q && k && vt && kmax && out, WANMI_ERR_ARG, "wanmi_attention_const_max: null pointer");
   WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_MX || out_scales, WANMI_ERR_ARG,
                 "wanmi_attention_const_max: MX output needs out_scales");
-  WANMI_REQUIRE(((Sq - 1) * q_token_stride + 128) * 2 < (1LL << 31) && ((Sk - 1) * k_token_stride + 128) * 2 < (1LL << 31) &&
+  // descriptors cover one wave's 32 queries, one 64-key tile, one head of V^T
+  WANMI_REQUIRE((31 * q_token_stride + 128) * 2 < (1LL << 31) && (63 * k_token_stride + 128) * 2 < (1LL << 31) &&
                     128 * vt_ld * 2 < (1LL << 31),
-                WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: per-head extent exceeds 2 GiB");
+                WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: strides too large for 32-bit buffer offsets");
   WANMI_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)vt % 16) == 0,
                 WANMI_ERR_ARG, "wanmi_attention_const_max: q/k/vt must be 16-byte aligned");
   AttnArgs a;
@@ -410,9 +428,15 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   a.out_scales = out_scales;
   a.os_ss = os_token_stride;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
+  const bool rebase_k = ((Sk - 1) * k_token_stride + 128) * 2 >= (1LL << 31);
   if (Sk <= 1024)
-    hipLaunchKernelGGL(attention_const_max_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(attention_const_max_kernel<true, false>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, a);
+  else if (!rebase_k)
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(attention_const_max_kernel<false, false>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(attention_const_max_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(attention_const_max_kernel<false, true>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, a);
   return check_launch("wanmi_attention_const_max");
 }
