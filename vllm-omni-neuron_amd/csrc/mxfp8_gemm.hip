@@ -180,17 +180,21 @@ __device__ __forceinline__ u32x4 maybe_empty(u32x4 r, bool valid) {
 // 64w .. 64w+63 of each operand tile, 8 rows (1 KiB) per instruction: in row group p (rows
 // 64w + 8p + (l >> 3)) lane l lands in physical 16-byte slot l & 7 and fetches the logical chunk
 // (l & 7) ^ f(row) = (l & 7) ^ (l >> 3) ^ (p & 1). The loads go in pairs (row group p of W and of
-// the activations) so they can be spread between MFMAs; lane offsets are recomputed per pair from
-// the lane id (a few VALU ops, which this kernel has to spare) rather than held in registers.
+// the activations) so they can be spread between MFMAs. Lane offsets are recomputed per pair from
+// the lane id (holding them across the MFMA block would spill operands), with one full-rate 24-bit
+// multiply-add per load (rows < 256; K and lda < 2^24, checked on the host) in place of a 64-bit
+// one. Token rows past M fall outside the activations' descriptor extent and read as zero.
 __device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
                                               int p, bool valid = true) {
-  const int l = fresh_lane_id();
-  const int srow = l >> 3;
-  const uint32_t col = (uint32_t)kt * BK + (uint32_t)((((l & 7) ^ srow ^ (p & 1))) << 4);
-  const uint32_t row = (uint32_t)(wave * 64 + p * 8 + srow);
-  const uint32_t lds = lds_addr(buf) + (uint32_t)(wave * 64 + p * 8) * BK;
-  lds_dma_b128(maybe_empty(t.w, valid), row * (uint32_t)g.K + col, lds);
-  lds_dma_b128(maybe_empty(t.a, valid), row * (uint32_t)g.lda + col, lds + TN * BK);
+  const uint32_t l = (uint32_t)fresh_lane_id();
+  const uint32_t srow = l >> 3;
+  const uint32_t col = ((l & 7) ^ srow ^ (uint32_t)(p & 1)) << 4;
+  const uint32_t kofs = (uint32_t)kt * BK;
+  const uint32_t rg = (uint32_t)(wave * 64 + p * 8);  // first row of the row group
+  const uint32_t lds = lds_addr(buf) + rg * BK;
+  const uint32_t row = srow + rg;
+  lds_dma_b128(maybe_empty(t.w, valid), (uint32_t)__umul24(row, (uint32_t)g.K) + col + kofs, lds);
+  lds_dma_b128(maybe_empty(t.a, valid), (uint32_t)__umul24(row, (uint32_t)g.lda) + col + kofs, lds + TN * BK);
 }
 
 __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
@@ -204,7 +208,8 @@ __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& 
 // queue (each moves 1 KiB) while its matrix pipe runs dry; spread out, each pair issues while an
 // MFMA executes. The scheduling barriers keep the compiler from regrouping them.
 __device__ __forceinline__ void mfma_all_with_dma(const SliceOperands& op, f32x16 (&acc)[4][4], const GemmArgs& g,
-                                                  const TileLoads& t, int kt, uint8_t* buf, int wave, bool valid) {
+                                                  const TileLoads& t, int kt, uint8_t* buf, int wave,
+                                                  bool valid) {
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int i = q >> 2, j = q & 3;
@@ -609,7 +614,8 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   WANMI_REQUIRE(tiles < (1LL << 31), WANMI_ERR_ARG, "wanmi_mxfp8_gemm: problem too large");
   WANMI_REQUIRE(M * ldo < (1LL << 32) && M < (1LL << 31), WANMI_ERR_UNSUPPORTED,
                 "wanmi_mxfp8_gemm: M=%lld x ldo=%lld output elements exceed 32-bit offsets", (long long)M, (long long)ldo);
-  // per-tile buffer offsets are 32-bit
+  // per-tile buffer offsets are 32-bit; this also keeps K and lda below 2^23 for the 24-bit
+  // multiplies of the load offsets
   WANMI_REQUIRE(TN * K < (1LL << 31) && TM * lda < (1LL << 31), WANMI_ERR_UNSUPPORTED,
                 "wanmi_mxfp8_gemm: K=%lld / lda=%lld too large", (long long)K, (long long)lda);
 
