@@ -15,7 +15,8 @@ wan2_2_transformer.py:1428-1513):
   quantization error is reported against.
 
 Weights come as the bf16 reference-layout dict of ``block.random_block_weights`` (``x @ W``) plus,
-for the MXFP8 path, their MX codes/scales in GEMM layout.
+for the MXFP8 path, their MX codes/scales in GEMM layout (optionally with a per-output-channel
+scale, the per-tensor FP8 checkpoint recipe).
 """
 
 from __future__ import annotations
@@ -45,9 +46,22 @@ def _mx_of(y: torch.Tensor):
     return omx.mx_quantize(y.float().numpy())
 
 
+def _proj(a_deq: torch.Tensor, wq) -> torch.Tensor:
+    """fp32 ``A_deq @ W_deq^T``, times the per-output-channel scale when ``wq`` carries one.
+
+    ``wq`` = (codes [N, K], scales [N, K/32]) for an MX weight, or (codes, scales, col_scale [N])
+    for a per-tensor FP8 checkpoint weight loaded with neutral block scales: the ROW_MX weight
+    dequant ``* c_i`` of qkv_cte.py:3996-4021 / row_mx_loaders.py:115-140, applied after the
+    accumulation as the GPU epilogue applies it."""
+    y = a_deq @ _deq(wq[0], wq[1]).T
+    if len(wq) > 2 and wq[2] is not None:
+        y = y * torch.as_tensor(np.asarray(wq[2], np.float32)).reshape(1, -1)
+    return y
+
+
 def _lin(a_codes, a_scales, wq, bias) -> torch.Tensor:
-    """bf16(A_deq @ W_deq^T + b), fp32 accumulation; ``wq`` = (codes [N, K], scales [N, K/32])."""
-    y = _deq(a_codes, a_scales) @ _deq(*wq).T + bias.float()
+    """bf16(A_deq @ W_deq^T [* col_scale] + b), fp32 accumulation; ``wq`` as in :func:`_proj`."""
+    y = _proj(_deq(a_codes, a_scales), wq) + bias.float()
     return _bf16(y)
 
 
@@ -97,7 +111,7 @@ def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6):
     r3 = oadaln.adaln_quant(attn2.numpy(), (1 + c_sc).numpy(), c_shift.numpy(), eps=eps, quant="mx",
                             residual=h1.numpy(), gate=None)
     h2 = torch.from_numpy(r3["residual_out"])
-    up = _deq(r3["codes"], r3["scales"]) @ _deq(*wq["up"]).T + raw["up_b"].float()
+    up = _proj(_deq(r3["codes"], r3["scales"]), wq["up"]) + raw["up_b"].float()
     g = torch.from_numpy(bf16_round(F.gelu(up, approximate="tanh").numpy()))
     gc, gs = _mx_of(g)
     ffn = _lin(gc, gs, wq["down"], raw["down_b"])

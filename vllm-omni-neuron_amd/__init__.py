@@ -22,3 +22,4 @@ from .attention_ops import (  # noqa: F401
     wan_cp_self_attention,
 )
 from . import block  # noqa: F401
+from . import comfy_fp8_checkpoint  # noqa: F401
