@@ -43,8 +43,12 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
+// Up to 40 heads (NCH <= 10) at most 128 VGPRs, four waves per SIMD: the 4095 waves of an S = 32760
+// launch (8 tokens each) are then resident in one round over 256 CUs; at the 130 VGPRs the compiler
+// would otherwise take, only three waves per SIMD fit and the last quarter of the grid runs as a
+// second round (190 vs 159 us). Wider rows keep the registers they need.
 template <int NCH>
-__global__ __launch_bounds__(256, 2) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
+__global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
