@@ -215,13 +215,11 @@ def main():
     gemm_names = [k for k in times if k.startswith("gemm_")]
     gemm_ms = sum(sum(times[k]) for k in gemm_names) / n_blk
     gemm_tflops = gemm_flops(S) / gemm_ms / 1e9
-    # adaLN: first launch of each block is the plain modulation (x read, MX codes + scales written);
-    # the second and third also read the residual and write the bf16 residual sum.
+    # adaLN: every launch reads x (bf16) and the two modulation / affine vectors and writes MX codes
+    # and scales (the residual adds run in the GEMM epilogues)
     plain = 2 * S * DIM + S * DIM + S * DIM // 32 + 2 * DIM * 4
-    fused = 2 * 2 * S * DIM + 2 * S * DIM + S * DIM + S * DIM // 32 + 3 * DIM * 4
     ad = times["adaln"]
-    ad_bytes = [plain if i % 3 == 0 else fused for i in range(len(ad))]
-    adaln_gbs = sum(ad_bytes) / sum(ad) / 1e6
+    adaln_gbs = plain * len(ad) / sum(ad) / 1e6
     first_adaln_us = sum(ad[0::3]) / len(ad[0::3]) * 1000.0
     comp = {k: {"ms_per_launch": round(sum(v) / len(v), 4), "ms_per_step": round(sum(v) / args.steps, 2)}
             for k, v in sorted(times.items())}

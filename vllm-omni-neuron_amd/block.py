@@ -8,10 +8,16 @@ wan2_2_transformer.py:1428-1513) with every projection in MXFP8 and attention in
     qkv = a1 @ Wqkv + b                               MXFP8 GEMM
     q, k = RoPE(RMS_heads(q) g_q), RoPE(RMS_heads(k) g_k); V^T      prep kernels
     o1 = MX(attention(q, k, v))                       constant-max attention, MX epilogue
-    h1, a2 = h + gate * (o1 @ Wo + b),  MX(LN_affine(h1))            GEMM + adaLN (fused residual)
+    h1 = h + gate * (o1 @ Wo + b);  a2 = MX(LN_affine(h1))          GEMM (gated residual) + adaLN
     q2 = RMS_heads(a2 @ Wq2 + b) g_q2; o2 = MX(attention(q2, K2, V2)) cross-attention (cached K2/V2)
-    h2, a3 = h1 + (o2 @ Wo2 + b),  MX(LN(h2) * (1 + c_scale) + c_shift)
+    h2 = h1 + (o2 @ Wo2 + b);  a3 = MX(LN(h2) * (1 + c_scale) + c_shift)    GEMM (residual) + adaLN
     h3 = h2 + c_gate * (MX(GELU_tanh(a3 @ Wup + b)) @ Wdown + b)     GEMM (GELU+MX) + GEMM (gated residual)
+
+Every residual add runs in the epilogue of the GEMM that produces the branch, as
+``bf16(residual + bf16(y) * gate)`` (fp32 product, then the sum; gate 1 for the cross-attention
+branch): the reference does the first two adds in its adaLN kernel (adaln_kernels.py:58-66 for the
+eager form) with the same fp32 product and sum of the bf16 branch output, so the results are the
+same bits, and the bf16 branch output never makes a round trip through HBM.
 
 The cross-attention K/V depend only on the text context, so -- as in the reference
 (``forward_and_cache_cross_attention_kv``, wan2_2_transformer.py:1675-1725) -- they are projected once
@@ -101,6 +107,17 @@ def project_cross_kv(w: BlockWeights, context: torch.Tensor, eps: float = 1e-6) 
     return CrossKV(k.view(-1, heads, HEAD_DIM), vt, kmax)
 
 
+_ONES: dict = {}
+
+
+def _ones(n: int, device) -> torch.Tensor:
+    """fp32 ones [n] on ``device`` (the gate of the ungated residual add), made once per device."""
+    key = (torch.device(device), n)
+    if key not in _ONES:
+        _ONES[key] = torch.ones(n, dtype=torch.float32, device=device)
+    return _ONES[key]
+
+
 def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cross: CrossKV,
                   eps: float = 1e-6, timer=None) -> torch.Tensor:
     """One block on ``h`` bf16 ``[S, DIM]``; ``temb`` ``[6, DIM]`` (or ``[1, 6, DIM]``); ``rope`` is
@@ -123,16 +140,15 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
     q = qkv[:, :dim].view(S, heads, HEAD_DIM)
     k = qkv[:, dim : 2 * dim].view(S, heads, HEAD_DIM)
     o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX))
-    attn1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o))
-    h1, a2 = run("adaln", lambda: adaln_quant_2d(attn1, w.norm2_weight, w.norm2_bias, eps=eps, norm_type="layer_norm",
-                                                quant="mx", residual=h, gate=gate))
+    h1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o, epilogue="gated_residual", residual=h, gate=gate))
+    a2 = run("adaln", lambda: adaln_quant_2d(h1, w.norm2_weight, w.norm2_bias, eps=eps, norm_type="layer_norm",
+                                             quant="mx"))
     q2 = run("gemm_q2", lambda: mxfp8_linear(a2, w.q2))
     run("qk_prep", lambda: ops.qk_rmsnorm_rope_(q2, w.norm_q2, eps=eps))
     o2 = run("cross_attention", lambda: ops.attention_core(q2.view(S, heads, HEAD_DIM), cross.k, cross.vt, cross.kmax,
                                                           scale, ops.OUT_MX))
-    attn2 = run("gemm_o2", lambda: mxfp8_linear(o2, w.o2))
-    h2, a3 = run("adaln", lambda: adaln_quant_2d(attn2, one_p_csc, c_shift, eps=eps, norm_type="layer_norm", quant="mx",
-                                                residual=h1, gate=None))
+    h2 = run("gemm_o2", lambda: mxfp8_linear(o2, w.o2, epilogue="gated_residual", residual=h1, gate=_ones(dim, h.device)))
+    a3 = run("adaln", lambda: adaln_quant_2d(h2, one_p_csc, c_shift, eps=eps, norm_type="layer_norm", quant="mx"))
     inter = run("gemm_up", lambda: mxfp8_linear(a3, w.up, epilogue="gelu_mx"))
     return run("gemm_down", lambda: mxfp8_linear(inter, w.down, epilogue="gated_residual", residual=h2, gate=c_gate))
 
