@@ -170,6 +170,28 @@ def test_self_attention_720p_rows(pkg, dev):
         _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
 
 
+def test_cross_attention_full_shape_rows(pkg, dev):
+    """Cross-attention of the step: 32760 video-token queries (normalized across heads, no RoPE) over
+    512 text keys, 40 heads, through the short-key instantiation; 96 query rows over three heads
+    (incl. the ragged last query block) against exact fp64 attention."""
+    ops = pkg.attention_ops
+    S, T, N = 32760, 512, 40
+    gdev = torch.Generator(device=dev).manual_seed(23)
+    q = torch.randn(S, N * 128, generator=gdev, device=dev).to(torch.bfloat16)
+    k = torch.randn(T, N * 128, generator=gdev, device=dev).to(torch.bfloat16)
+    v = torch.randn(T, N, 128, generator=gdev, device=dev).to(torch.bfloat16)
+    gamma = torch.ones(N * 128, device=dev)
+    ops.qk_rmsnorm_rope_(q, gamma)
+    kmax = ops.qk_rmsnorm_rope_(k, gamma, want_max=True)
+    q, k = q.view(S, N, 128), k.view(T, N, 128)
+    vt, _ = ops.transpose_heads(v)
+    out = ops.attention_core(q, k, vt, kmax, 128**-0.5)
+    rows = torch.tensor([0, 1, 255, 256, 16000, 32511, 32512, 32759] + list(range(20000, 20088)))[:96]
+    for h in (0, 21, 39):
+        ref = oa.torch_attend(q[rows, h].cpu(), k[:, h].cpu(), v[:, h].cpu(), 128**-0.5, dtype=torch.float64)
+        _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
+
+
 def test_dropins_match_reference_layouts(pkg, dev):
     ops = pkg.attention_ops
     B, N, S, D = 1, 4, 200, 128

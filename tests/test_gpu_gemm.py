@@ -124,6 +124,26 @@ def test_gemm_full_qkv_shape_row_subset(pkg, dev):
     _check(y[rows].cpu(), og.mx_gemm(*ops), og.abs_gemm(*ops))
 
 
+def test_gemm_720p_qkv_shape_row_subset(pkg, dev):
+    """QKV projection of the 720p step, [75600, 5120] x [5120, 15360] (the 15360-wide bf16 output is
+    2.3 GB); 48 rows (incl. the ragged last tile) against the fp64 oracle."""
+    M, N, K = 75600, 15360, 5120
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(K, N, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g, device=dev) * 0.1
+    xq = pkg.adaln_modulate(x, eps=0.0, norm_type="none", quant="mx")
+    del x
+    wq = pkg.quantize_weight_mx(w, b)
+    y = pkg.mxfp8_linear(xq, wq)
+    rows = torch.tensor([0, 1, 255, 256, 37800, 75263, 75264, 75265] + list(range(75560, 75600)), device=dev)
+    ops = (
+        xq.codes.view(torch.uint8)[rows].cpu().numpy(), xq.scales[rows].cpu().numpy(),
+        wq.codes.view(torch.uint8).cpu().numpy(), wq.scales.cpu().numpy(),
+    )
+    _check(y[rows].cpu(), og.mx_gemm(*ops, bias=b.cpu().numpy()), og.abs_gemm(*ops) + 1e-3)
+
+
 def test_gemm_rejects_unsupported_shapes(pkg, dev):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(64, 256, generator=g).to(torch.bfloat16).to(dev)
