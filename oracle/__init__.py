@@ -2,17 +2,18 @@
 
 A restatement, in numpy / torch-on-CPU, of the reference's arithmetic for this path
 (reecedantin/vllm-omni-neuron). Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-CPU-baseline leg may import it, and only as the checker or the reported CPU baseline; the product
-package never imports it and has no CPU fallback.
+CPU-baseline leg may import it, and only to check results or as the reported CPU baseline; the
+product package never imports it and has no CPU fallback.
 
-Modules and what pins each (full table in DESIGN.md):
+Modules and what pins each:
 
 - ``fp8``: e4m3fn / bf16 rounding and e8m0 scales, bit level. Pinned against torch's own
   float8_e4m3fn and bfloat16 casts on every bf16 bit pattern plus random fp32 and ties.
 - ``mx``: MX block quantization (shared exponent = block max - 7) and ROW packing. Pinned by
   known-answer blocks whose codes follow from the rule by hand, and by dequantization bounds.
-- ``adaln``: the canonical fused adaLN (exact fixed-grid statistics). Pinned against
-  ``math.fsum`` sums, ``F.layer_norm`` / eager restatement distance, and LayerNorm invariants.
+- ``adaln``: the canonical fused adaLN (fixed-order fp32 row statistics in the kernel's lane
+  order). Pinned against ``math.fsum`` sums within the fp32 error bound, the distance to
+  ``F.layer_norm`` / the eager restatement, and LayerNorm invariants.
 - ``rope``: Wan 3D RoPE tables and interleaved rotation. Pinned by norm preservation, the
   rotate-half equivalence and closed-form angles.
 - ``attention``: exact softmax attention and the constant-max form. Pinned by fp64 brute force,
