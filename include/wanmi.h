@@ -88,6 +88,20 @@ int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales, const uint
                      const float* gate, void* stream);
 
 /*
+ * wanmi_mxfp8_gemm with the bf16 epilogue, which also writes per-row partial sums of squares of
+ * the bf16 outputs: row_sumsq[m * (N/128) + b] = sum over the 128 columns of block b of out[m, c]^2
+ * (fp32), for the blocks of columns [0, sumsq_cols) (sumsq_cols % 128 == 0). The across-heads
+ * RMSNorm of the projected Q then needs no pass over Q: the attention kernel's Q load sums the
+ * row's partials (wanmi_attention_const_max_qprep). Replaces the sum of squares the reference's
+ * QKV kernel takes from its bf16 output tile (kernels/nkilib/core/qkv/qkv_cte.py:3781-3801).
+ */
+int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                              const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                              const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda,
+                              void* out, int64_t ldo, float* row_sumsq, int64_t sumsq_cols,
+                              void* stream);
+
+/*
  * Across-heads RMSNorm + optional interleaved 3D RoPE, in place on a bf16 [S, heads*128] slab
  * (row stride ld elements):  x = bf16(x * rrms * gamma), rrms = 1/sqrt(mean_row(x^2) + eps);
  * then per pair (2i, 2i+1) of each head: (a, b) -> bf16(a cos - b sin), bf16(a sin + b cos) with
@@ -142,6 +156,26 @@ int wanmi_attention_const_max(const void* q, int64_t q_head_stride, int64_t q_to
                               void* out, int64_t o_head_stride, int64_t o_token_stride,
                               int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
                               void* stream);
+
+/*
+ * wanmi_attention_const_max with the Q preparation fused into the kernel's Q load: q holds the raw
+ * projection, and each query is normalized across heads, then optionally rotated, before use:
+ *   q_hat = bf16(bf16(q * rrms * q_gamma) rotated),  rrms = 1/sqrt(sum_b q_sumsq[s, b] / (heads*128) + q_eps)
+ * q_sumsq: [Sq, q_sumsq_ld] fp32 per-128-column partial sums of squares of the row (heads blocks,
+ * summed in block order; from wanmi_mxfp8_gemm_rowsumsq); q_gamma: fp32 [heads*128]; q_cos, q_sin:
+ * fp32 [Sq, 64] pair tables or both NULL (no RoPE). heads % 4 == 0.
+ * Replaces DistributedRMSNorm + apply_rotary_emb_wan on Q (vllm_omni_neuron/diffusion/models/
+ * wan2_2/wan2_2_transformer.py:879-893, diffusion/layers/rope.py:8-34) and the normalize-and-rotate
+ * epilogue of the reference's QKV kernel (kernels/nkilib/core/qkv/qkv_cte.py:3870-3990).
+ */
+int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                    const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                    const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                    int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                    void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                    int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                    const float* q_sumsq, int64_t q_sumsq_ld, const float* q_gamma,
+                                    const float* q_cos, const float* q_sin, float q_eps, void* stream);
 
 /*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,

@@ -192,6 +192,41 @@ def test_cross_attention_full_shape_rows(pkg, dev):
         _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
 
 
+@pytest.mark.parametrize("with_rope", [True, False])
+def test_attention_with_q_prepared_on_load(pkg, dev, with_rope):
+    """q raw, the across-heads RMSNorm (+ RoPE) applied in the attention's Q load from per-head
+    partial sums of squares: against exact fp64 attention over the oracle-prepared q, and close to
+    the separate-pass path (same operations; only the order of the row sum differs)."""
+    ops = pkg.attention_ops
+    Sq, Sk, N = 300, 200, 4
+    grid = (1, 10, 30)
+    g = torch.Generator().manual_seed(33)
+    q = torch.randn(Sq, N * 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    gamma = 1 + 0.1 * torch.randn(N * 128, generator=g)
+    cos, sin = orope.wan_rope(grid)
+    c64, s64 = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    qd, kd = q.to(dev), k.to(dev)
+    vt, _ = ops.transpose_heads(v.to(dev))
+    kmax = ops.head_max_norm(kd)
+    sumsq = q.float().pow(2).view(Sq, N, 128).sum(-1).to(dev)
+    prep = ops.QPrep(sumsq, gamma.to(dev), c64 if with_rope else None, s64 if with_rope else None, 1e-6)
+    out = ops.attention_core(qd.view(Sq, N, 128), kd, vt, kmax, 128**-0.5, q_prep=prep).cpu()
+    qn = orope.rms_norm_across_heads(q, gamma).view(1, Sq, N, 128)
+    if with_rope:
+        qn = orope.apply_rotary_emb_wan(qn, cos[None, :, None], sin[None, :, None])
+    qn = qn.view(Sq, N, 128).to(torch.bfloat16)
+    for h in range(N):
+        ref = oa.torch_attend(qn[:, h], k[:, h], v[:, h], 128**-0.5, dtype=torch.float64)
+        _check_attn(out.view(Sq, N, 128)[:, h], ref)
+    q2 = qd.clone()
+    ops.qk_rmsnorm_rope_(q2, gamma.to(dev), cos=c64 if with_rope else None, sin=s64 if with_rope else None)
+    two_pass = ops.attention_core(q2.view(Sq, N, 128), kd, vt, kmax, 128**-0.5).cpu()
+    diff = (out.float() - two_pass.float()).abs().max() / two_pass.float().abs().max()
+    assert diff <= 1e-2, diff
+
+
 def test_dropins_match_reference_layouts(pkg, dev):
     ops = pkg.attention_ops
     B, N, S, D = 1, 4, 200, 128

@@ -133,17 +133,21 @@ def test_block_stagewise(pkg, dev, run):
     # QKV projection from the GPU's a1
     qkv_pre = snap["gemm_qkv"][0].cpu()
     _close(qkv_pre, oblock._lin(*_mx_np(a1), wq["qkv"], raw["qkv_b"]), "qkv projection")
-    # Q/K RMSNorm + RoPE from the GPU's projection
+    # Q/K RMSNorm + RoPE from the GPU's projection: K in place (its own pass), Q inside the attention
     qkv_post = live["gemm_qkv"][0].cpu()
+    refn = {}
     for part, gname in ((0, "norm_q"), (1, "norm_k")):
         x = qkv_pre[:, part * dim : (part + 1) * dim].to(torch.bfloat16)
-        refn = orope.rms_norm_across_heads(x, raw[gname]).view(1, S, heads, D)
-        refn = orope.apply_rotary_emb_wan(refn, r["cos"][None, :, None], r["sin"][None, :, None]).view(S, dim)
-        _close(qkv_post[:, part * dim : (part + 1) * dim], refn, f"{gname} + RoPE")
-    # self-attention from the GPU's q, k, v
-    q, k, v = (qkv_post[:, i * dim : (i + 1) * dim].view(S, heads, D) for i in range(3))
+        rn = orope.rms_norm_across_heads(x, raw[gname]).view(1, S, heads, D)
+        refn[gname] = orope.apply_rotary_emb_wan(rn, r["cos"][None, :, None], r["sin"][None, :, None]).view(S, dim)
+    _close(qkv_post[:, dim : 2 * dim], refn["norm_k"], "norm_k + RoPE")
+    assert torch.equal(qkv_post[:, :dim], qkv_pre[:, :dim].to(torch.bfloat16)), "Q must stay the raw projection"
+    # self-attention from the GPU's raw q (normalized + rotated on load), k, v, against the oracle's
+    # attention over the oracle-prepared q
+    k, v = (qkv_post[:, i * dim : (i + 1) * dim].view(S, heads, D) for i in (1, 2))
     o1 = snap["self_attention"][0]
-    _mx_close(o1, oblock._attend(q, k, v, s), "self-attention (MX out)")
+    _mx_close(o1, oblock._attend(refn["norm_q"].to(torch.bfloat16).view(S, heads, D), k, v, s),
+              "self-attention with Q RMSNorm+RoPE on load (MX out)")
     # o-proj with the gated residual in its epilogue, from the GPU's MX attention output:
     # h1 = bf16(h + bf16(o1 @ Wo + b) * gate)
     h1 = snap["gemm_o"][0].cpu()
@@ -166,8 +170,7 @@ def test_block_stagewise(pkg, dev, run):
     # cross-attention query projection + RMSNorm
     q2_pre = snap["gemm_q2"][0].cpu()
     _close(q2_pre, oblock._lin(*_mx_np(a2), wq["q2"], raw["q2_b"]), "cross q projection")
-    q2 = live["gemm_q2"][0].cpu()
-    _close(q2, orope.rms_norm_across_heads(q2_pre.to(torch.bfloat16), raw["norm_q2"]), "cross q RMSNorm")
+    q2 = orope.rms_norm_across_heads(q2_pre.to(torch.bfloat16), raw["norm_q2"])
     # cached cross K/V vs the oracle's projection of the same context
     cc, cs = omx.mx_quantize(r["ctx"].float().numpy())
     k2 = orope.rms_norm_across_heads(oblock._lin(cc, cs, wq["k2"], raw["k2_b"]).to(torch.bfloat16), raw["norm_k2"])

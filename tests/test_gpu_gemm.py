@@ -144,6 +144,24 @@ def test_gemm_720p_qkv_shape_row_subset(pkg, dev):
     _check(y[rows].cpu(), og.mx_gemm(*ops, bias=b.cpu().numpy()), og.abs_gemm(*ops) + 1e-3)
 
 
+def test_gemm_row_sumsq(pkg, dev):
+    """bf16 epilogue with per-row partial sums of squares: out is bit-identical to the plain GEMM,
+    row_sumsq[:, b] equals the fp64 sum of the squared bf16 outputs of column block b (to fp32
+    summation error) for the blocks below sumsq_cols, and the other blocks are not written."""
+    M, N, K = 300, 768, 640
+    xq, wq, ops, b = _operands(pkg, dev, M, N, K, seed=5)
+    y = pkg.mxfp8_linear(xq, wq)
+    rs = torch.full((M, N // 128), float("nan"), device=dev)
+    y2 = pkg.mxfp8_linear(xq, wq, row_sumsq=rs, sumsq_cols=512)
+    assert torch.equal(y, y2)
+    ref = y.double().cpu().pow(2).view(M, N // 128, 128).sum(-1)
+    got = rs.cpu().double()
+    assert torch.allclose(got[:, :4], ref[:, :4], rtol=2e-5, atol=0.0), (got[:, :4] - ref[:, :4]).abs().max()
+    assert bool(torch.isnan(got[:, 4:]).all())
+    with pytest.raises(ValueError, match="multiple of 128"):
+        pkg.mxfp8_linear(xq, wq, row_sumsq=rs, sumsq_cols=100)
+
+
 def test_gemm_rejects_unsupported_shapes(pkg, dev):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(64, 256, generator=g).to(torch.bfloat16).to(dev)

@@ -36,9 +36,14 @@ _SIGNATURES = {
     "wanmi_qk_rmsnorm_rope": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _f32, _vp, _vp],
     "wanmi_transpose_heads": [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "wanmi_head_max_norm": [_vp, _i64, _i64, _i64, _i32, _vp, _vp],
+    "wanmi_mxfp8_gemm_rowsumsq": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
     "wanmi_attention_const_max": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _i64, _vp,
+    ],
+    "wanmi_attention_const_max_qprep": [
+        _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
+        _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _f32, _vp,
     ],
 }
 

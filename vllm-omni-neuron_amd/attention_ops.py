@@ -19,6 +19,8 @@ All attention here is the constant-max form (exact softmax by shift invariance, 
 
 from __future__ import annotations
 
+from typing import NamedTuple
+
 import math
 
 import torch
@@ -91,11 +93,26 @@ def head_max_norm(k: torch.Tensor) -> torch.Tensor:
     return out
 
 
+class QPrep(NamedTuple):
+    """Q preparation fused into the attention's Q load: ``sumsq`` fp32 ``[Sq, >= N]`` per-128-column
+    partial sums of squares of the raw q rows (from ``mxfp8_linear(..., row_sumsq=...)``), ``gamma``
+    fp32 ``[N*128]`` (the across-heads RMSNorm weight), optional RoPE pair tables ``cos``/``sin``
+    fp32 ``[Sq, 64]``, and the norm's ``eps``."""
+
+    sumsq: torch.Tensor
+    gamma: torch.Tensor
+    cos: torch.Tensor | None = None
+    sin: torch.Tensor | None = None
+    eps: float = 1e-6
+
+
 def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: torch.Tensor, scale: float,
-                   out_mode: int = OUT_TOKEN, out: torch.Tensor | None = None):
+                   out_mode: int = OUT_TOKEN, out: torch.Tensor | None = None, q_prep: QPrep | None = None):
     """Constant-max attention on ``[S, N, 128]`` views q (Sq) and k (Sk), V^T from
     :func:`transpose_heads`. Returns token-major bf16 ``[Sq, N*128]``, d-major bf16
-    ``[N, 128, Sq]`` or an :class:`MXTensor` ``[Sq, N*128]``."""
+    ``[N, 128, Sq]`` or an :class:`MXTensor` ``[Sq, N*128]``. With ``q_prep`` q is the raw
+    projection and the kernel applies the across-heads RMSNorm (and RoPE) to it on load, exactly as
+    :func:`qk_rmsnorm_rope_` would in a separate pass."""
     lib = _lib.load()
     _lib.require_gpu(q, k, vt, kmax, what="attention")
     Sq, N, D = q.shape
@@ -114,12 +131,25 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
         out = torch.empty((Sq, N * D), dtype=torch.uint8, device=dev) if out is None else out
         scales = torch.empty((Sq, N * D // 32), dtype=torch.uint8, device=dev)
         o_hs, o_ss, o_ds = D, out.stride(0), 1
-    st = lib.wanmi_attention_const_max(
+    common = (
         _lib.ptr(q), q.stride(1), q.stride(0), _lib.ptr(k), k.stride(1), k.stride(0), _lib.ptr(vt),
         vt.shape[-1], _lib.ptr(kmax), Sq, Sk, N, D, float(scale), out_mode, _lib.ptr(out), o_hs, o_ss, o_ds,
-        _lib.ptr(scales), 0 if scales is None else scales.stride(0), _lib.stream_of(q),
+        _lib.ptr(scales), 0 if scales is None else scales.stride(0),
     )
-    _lib.check(st, "wanmi_attention_const_max")
+    if q_prep is None:
+        st = lib.wanmi_attention_const_max(*common, _lib.stream_of(q))
+        _lib.check(st, "wanmi_attention_const_max")
+    else:
+        ss = q_prep.sumsq
+        _lib.require_gpu(ss, q_prep.gamma, q_prep.cos, q_prep.sin, what="attention")
+        if ss.dim() != 2 or ss.shape[0] != Sq or ss.stride(1) != 1 or ss.dtype != torch.float32:
+            raise ValueError("q_prep.sumsq must be fp32 [Sq, blocks] with unit column stride")
+        gamma = q_prep.gamma.reshape(-1).to(torch.float32).contiguous()
+        st = lib.wanmi_attention_const_max_qprep(
+            *common, _lib.ptr(ss), ss.stride(0), _lib.ptr(gamma), _lib.ptr(q_prep.cos), _lib.ptr(q_prep.sin),
+            float(q_prep.eps), _lib.stream_of(q),
+        )
+        _lib.check(st, "wanmi_attention_const_max_qprep")
     if out_mode == OUT_MX:
         return MXTensor(out.view(torch.float8_e4m3fn), scales)
     return out

@@ -5,11 +5,11 @@ wan2_2_transformer.py:1428-1513) with every projection in MXFP8 and attention in
 
     e = scale_shift_table + temb                     -> shift, scale, gate, c_shift, c_scale, c_gate
     a1 = MX(LN(h) * (1 + scale) + shift)              adaLN kernel
-    qkv = a1 @ Wqkv + b                               MXFP8 GEMM
-    q, k = RoPE(RMS_heads(q) g_q), RoPE(RMS_heads(k) g_k); V^T      prep kernels
-    o1 = MX(attention(q, k, v))                       constant-max attention, MX epilogue
+    qkv = a1 @ Wqkv + b                               MXFP8 GEMM (+ per-row sums of q^2 per 128 columns)
+    k = RoPE(RMS_heads(k) g_k), max||k||; V^T         prep kernels
+    o1 = MX(attention(RoPE(RMS_heads(q) g_q), k, v))  constant-max attention, Q prepared on load, MX out
     h1 = h + gate * (o1 @ Wo + b);  a2 = MX(LN_affine(h1))          GEMM (gated residual) + adaLN
-    q2 = RMS_heads(a2 @ Wq2 + b) g_q2; o2 = MX(attention(q2, K2, V2)) cross-attention (cached K2/V2)
+    o2 = MX(attention(RMS_heads(a2 @ Wq2 + b) g_q2, K2, V2))    GEMM (+ sums of q2^2) + cross-attention
     h2 = h1 + (o2 @ Wo2 + b);  a3 = MX(LN(h2) * (1 + c_scale) + c_shift)    GEMM (residual) + adaLN
     h3 = h2 + c_gate * (MX(GELU_tanh(a3 @ Wup + b)) @ Wdown + b)     GEMM (GELU+MX) + GEMM (gated residual)
 
@@ -132,21 +132,25 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
     cos, sin = rope
 
     a1 = run("adaln", lambda: adaln_quant_2d(h, one_p_sc, shift, eps=eps, norm_type="layer_norm", quant="mx"))
-    qkv = run("gemm_qkv", lambda: mxfp8_linear(a1, w.qkv))
-    run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qkv[:, :dim], w.norm_q, cos=cos, sin=sin, eps=eps))
+    # The Q rows' sums of squares come out of the QKV GEMM's epilogue (blocks 0 .. heads-1 of the
+    # 128-column blocks); the attention normalizes and rotates Q as it loads it. K is prepared in a
+    # pass of its own: the key-norm bound needs max ||k|| over all keys before the attention starts.
+    q_ss = torch.empty((S, 3 * dim // 128), dtype=torch.float32, device=h.device)
+    qkv = run("gemm_qkv", lambda: mxfp8_linear(a1, w.qkv, row_sumsq=q_ss, sumsq_cols=dim))
     kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qkv[:, dim : 2 * dim], w.norm_k, cos=cos, sin=sin, eps=eps,
                                                       want_max=True))
     vt, _ = run("v_transpose", lambda: ops.transpose_heads(qkv[:, 2 * dim :].view(S, heads, HEAD_DIM)))
     q = qkv[:, :dim].view(S, heads, HEAD_DIM)
     k = qkv[:, dim : 2 * dim].view(S, heads, HEAD_DIM)
-    o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX))
+    o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX,
+                                                         q_prep=ops.QPrep(q_ss, w.norm_q, cos, sin, eps)))
     h1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o, epilogue="gated_residual", residual=h, gate=gate))
     a2 = run("adaln", lambda: adaln_quant_2d(h1, w.norm2_weight, w.norm2_bias, eps=eps, norm_type="layer_norm",
                                              quant="mx"))
-    q2 = run("gemm_q2", lambda: mxfp8_linear(a2, w.q2))
-    run("qk_prep", lambda: ops.qk_rmsnorm_rope_(q2, w.norm_q2, eps=eps))
+    q2_ss = torch.empty((S, dim // 128), dtype=torch.float32, device=h.device)
+    q2 = run("gemm_q2", lambda: mxfp8_linear(a2, w.q2, row_sumsq=q2_ss, sumsq_cols=dim))
     o2 = run("cross_attention", lambda: ops.attention_core(q2.view(S, heads, HEAD_DIM), cross.k, cross.vt, cross.kmax,
-                                                          scale, ops.OUT_MX))
+                                                          scale, ops.OUT_MX, q_prep=ops.QPrep(q2_ss, w.norm_q2, eps=eps)))
     h2 = run("gemm_o2", lambda: mxfp8_linear(o2, w.o2, epilogue="gated_residual", residual=h1, gate=_ones(dim, h.device)))
     a3 = run("adaln", lambda: adaln_quant_2d(h2, one_p_csc, c_shift, eps=eps, norm_type="layer_norm", quant="mx"))
     inter = run("gemm_up", lambda: mxfp8_linear(a3, w.up, epilogue="gelu_mx"))

@@ -51,6 +51,15 @@ struct AttnArgs {
   int64_t o_hs, o_ss, o_ds;  // token-major: (h, s, d) at o_hs*h + o_ss*s + d; d-major: + o_ds*d + s
   uint8_t* out_scales;       // MX: [Sq, heads*4] at (s, h*4 + dtile)
   int64_t os_ss;
+  // Fused Q preparation (q_sumsq non-null): q holds the raw projection, and the kernel applies the
+  // across-heads RMSNorm (from per-128-column partial sums of squares, [Sq, qss_ld], blocks in
+  // order) with q_gamma [heads*128] and, if q_cos is given, the interleaved RoPE ([Sq, 64] tables).
+  const float* q_sumsq;
+  int64_t qss_ld;
+  const float* q_gamma;
+  const float* q_cos;
+  const float* q_sin;
+  float q_eps;
 };
 
 // LDS tiles, a ring of kStages (tile t in slot t % kStages):
@@ -201,11 +210,72 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   const int64_t qvalid = a.Sq - q0 < 32 ? (a.Sq - q0 > 0 ? a.Sq - q0 : 0) : 32;
   const __amdgpu_buffer_rsrc_t r_q =
       attn_rsrc(a.q + h * a.q_hs + (qvalid > 0 ? q0 * a.q_ss : 0), qvalid > 0 ? ((qvalid - 1) * a.q_ss + 128) * 2 : 0);
+  // fused Q preparation: the query's across-heads 1/rms from its partial sums, in block order
+  const bool qprep = a.q_sumsq != nullptr;
+  float rr = 1.0f;
+  if (qprep) {
+    const __amdgpu_buffer_rsrc_t r_ss = attn_rsrc(a.q_sumsq + (qvalid > 0 ? q0 * a.qss_ld : 0),
+                                                  qvalid > 0 ? ((qvalid - 1) * a.qss_ld + a.heads) * 4 : 0);
+    float ss = 0.0f;
+    if (a.heads <= 40) {
+      // all loads first (a dependent loop would pay one load latency per 4 blocks); blocks past
+      // `heads` read as zero and add exactly nothing, so the sum is the block-ordered one
+      u32x4 pv[10];
+#pragma unroll
+      for (int i = 0; i < 10; ++i)
+        pv[i] = 4 * i < a.heads
+                    ? __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + 4 * i) * 4), 0, 0)
+                    : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 10; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = ss + __uint_as_float(pv[i][j]);
+    } else {
+      for (int b4 = 0; b4 < a.heads; b4 += 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + b4) * 4), 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = ss + __uint_as_float(v[j]);
+      }
+    }
+    rr = (float)(1.0 / sqrt((double)(ss / (float)(a.heads * 128)) + (double)a.q_eps));
+  }
+  const __amdgpu_buffer_rsrc_t r_gm = attn_rsrc(qprep ? a.q_gamma + h * 128 : nullptr, qprep ? 128 * 4 : 0);
+  const bool qrope = qprep && a.q_cos != nullptr;
+  const __amdgpu_buffer_rsrc_t r_cs =
+      attn_rsrc(qrope ? a.q_cos + (qvalid > 0 ? q0 * 64 : 0) : nullptr, qrope && qvalid > 0 ? qvalid * 64 * 4 : 0);
+  const __amdgpu_buffer_rsrc_t r_sn =
+      attn_rsrc(qrope ? a.q_sin + (qvalid > 0 ? q0 * 64 : 0) : nullptr, qrope && qvalid > 0 ? qvalid * 64 * 4 : 0);
   bf16x8 qf[8];
   float qn2 = 0.0f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+    if (qprep) {
+      // x_hat = bf16((x rrms) gamma), then the pair rotation (a cos - b sin, a sin + b cos) -> bf16:
+      // the same operations, in the same order, as the separate Q/K preparation pass
+      const u32x4 g0 = __builtin_amdgcn_raw_buffer_load_b128(r_gm, (uint32_t)((16 * t + 8 * hq) * 4), 0, 0);
+      const u32x4 g1 = __builtin_amdgcn_raw_buffer_load_b128(r_gm, (uint32_t)((16 * t + 8 * hq + 4) * 4), 0, 0);
+      const float gv[8] = {__uint_as_float(g0[0]), __uint_as_float(g0[1]), __uint_as_float(g0[2]),
+                           __uint_as_float(g0[3]), __uint_as_float(g1[0]), __uint_as_float(g1[1]),
+                           __uint_as_float(g1[2]), __uint_as_float(g1[3])};
+      u32x4 cv = {0u, 0u, 0u, 0u}, sv = {0u, 0u, 0u, 0u};
+      if (qrope) {
+        cv = __builtin_amdgcn_raw_buffer_load_b128(r_cs, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
+        sv = __builtin_amdgcn_raw_buffer_load_b128(r_sn, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float a0 = round_bf16((bf16_lo(v[j]) * rr) * gv[2 * j]);
+        float b0 = round_bf16((bf16_hi(v[j]) * rr) * gv[2 * j + 1]);
+        if (qrope) {
+          const float c = __uint_as_float(cv[j]), sn = __uint_as_float(sv[j]);
+          const float ac = a0 * c, bs = b0 * sn, as = a0 * sn, bc = b0 * c;
+          a0 = ac - bs;
+          b0 = as + bc;
+        }
+        v[j] = pack_bf16x2(a0, b0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float lo = bf16_lo(v[j]), hi = bf16_hi(v[j]);
@@ -375,15 +445,22 @@ extern "C" int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t t
   return check_launch("wanmi_head_max_norm");
 }
 
-extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, int64_t q_token_stride,
-                                         const void* k, int64_t k_head_stride, int64_t k_token_stride,
-                                         const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
-                                         int64_t Sk, int heads, int head_dim, float scale, int out_mode,
-                                         void* out, int64_t o_head_stride, int64_t o_token_stride,
-                                         int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
-                                         void* stream) {
-  using namespace wanmi;
-  clear_error();
+namespace wanmi {
+struct QPrep {
+  const float* sumsq = nullptr;
+  int64_t ld = 0;
+  const float* gamma = nullptr;
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  float eps = 0.0f;
+};
+
+static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_stride, const void* k,
+                          int64_t k_head_stride, int64_t k_token_stride, const void* vt, int64_t vt_ld,
+                          const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
+                          int out_mode, void* out, int64_t o_head_stride, int64_t o_token_stride,
+                          int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride, const QPrep& qp,
+                          void* stream) {
   WANMI_REQUIRE(head_dim == 128, WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: head_dim must be 128, got %d",
                 head_dim);
   WANMI_REQUIRE(Sq >= 0 && Sk > 0 && heads > 0 && heads <= 65535, WANMI_ERR_ARG,
@@ -427,6 +504,12 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   a.o_ds = o_d_stride;
   a.out_scales = out_scales;
   a.os_ss = os_token_stride;
+  a.q_sumsq = qp.sumsq;
+  a.qss_ld = qp.ld;
+  a.q_gamma = qp.gamma;
+  a.q_cos = qp.cos;
+  a.q_sin = qp.sin;
+  a.q_eps = qp.eps;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
   const bool rebase_k = ((Sk - 1) * k_token_stride + 128) * 2 >= (1LL << 31);
   if (Sk <= 1024)
@@ -439,4 +522,52 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
     hipLaunchKernelGGL(HIP_KERNEL_NAME(attention_const_max_kernel<false, true>), grid, dim3(kThreads), 0,
                        (hipStream_t)stream, a);
   return check_launch("wanmi_attention_const_max");
+}
+}  // namespace wanmi
+
+extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                         const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                         const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                         int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                         void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                         int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                         void* stream) {
+  wanmi::clear_error();
+  return wanmi::attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq,
+                               Sk, heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride,
+                               out_scales, os_token_stride, wanmi::QPrep{}, stream);
+}
+
+extern "C" int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                               const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                               const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                               int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                               void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                               int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                               const float* q_sumsq, int64_t q_sumsq_ld, const float* q_gamma,
+                                               const float* q_cos, const float* q_sin, float q_eps, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(q_sumsq && q_gamma, WANMI_ERR_ARG, "wanmi_attention_const_max_qprep: q_sumsq and q_gamma are required");
+  WANMI_REQUIRE((q_cos == nullptr) == (q_sin == nullptr), WANMI_ERR_ARG,
+                "wanmi_attention_const_max_qprep: q_cos and q_sin must both be given or both be null");
+  WANMI_REQUIRE(heads % 4 == 0 && q_sumsq_ld >= heads && q_sumsq_ld % 4 == 0, WANMI_ERR_ARG,
+                "wanmi_attention_const_max_qprep: need heads %% 4 == 0 and q_sumsq_ld >= heads, a multiple of 4 "
+                "(heads=%d, ld=%lld)", heads, (long long)q_sumsq_ld);
+  WANMI_REQUIRE(!(q_eps < 0.0f), WANMI_ERR_ARG, "wanmi_attention_const_max_qprep: eps must be >= 0");
+  WANMI_REQUIRE(((uintptr_t)q_sumsq % 16) == 0 && ((uintptr_t)q_gamma % 16) == 0 &&
+                    (!q_cos || (((uintptr_t)q_cos % 16) == 0 && ((uintptr_t)q_sin % 16) == 0)),
+                WANMI_ERR_ARG, "wanmi_attention_const_max_qprep: q_sumsq, q_gamma, q_cos, q_sin must be 16-byte aligned");
+  WANMI_REQUIRE((31 * q_sumsq_ld + heads) * 4 < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+                "wanmi_attention_const_max_qprep: q_sumsq_ld too large");
+  QPrep qp;
+  qp.sumsq = q_sumsq;
+  qp.ld = q_sumsq_ld;
+  qp.gamma = q_gamma;
+  qp.cos = q_cos;
+  qp.sin = q_sin;
+  qp.eps = q_eps;
+  return attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq, Sk,
+                        heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride, out_scales,
+                        os_token_stride, qp, stream);
 }

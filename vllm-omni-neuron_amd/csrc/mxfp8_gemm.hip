@@ -67,6 +67,8 @@ struct GemmArgs {
   const float* gate;        // [N]
   void* out;                // [M, ldo]
   uint8_t* out_scales;      // [M, N/32]
+  float* row_sumsq;         // [M, N/128]: sum of squares of the bf16 outputs per 128-column block, or null
+  int64_t sumsq_cols;       // blocks of columns [0, sumsq_cols) are summed
   int64_t M, N, K, lda, ldo;
   int tiles_m, tiles_n;
 };
@@ -329,6 +331,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       const int j = 2 * hf + jj;
       const int tok = jj * 32 + r32;  // token within the half
       [[maybe_unused]] uint32_t sbytes = 0;
+      // bf16 epilogue with row_sumsq: this lane's part of the token's sum of squares of the rounded
+      // outputs over the wave's 128 columns (features 32 i + 8 gi + 4 h + q, in that order)
+      [[maybe_unused]] float ss = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v[16];
@@ -361,9 +366,28 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
               y[q] = EPI == WANMI_EPI_GELU_BF16 ? gelu_tanh(x) : x;  // gated residual: bf16(v) here
             }
             // features 32 i + 8 gi + 4 h .. +3: chunk 4 i + gi, byte 8 h
-            *reinterpret_cast<uint2*>(stage + stg16(tok, 4 * i + gi) + 8 * h) =
-                make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+            const uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
+            *reinterpret_cast<uint2*>(stage + stg16(tok, 4 * i + gi) + 8 * h) = make_uint2(p0, p1);
+            if constexpr (EPI == WANMI_EPI_BF16) {
+              if (g.row_sumsq) {
+                const float b[4] = {bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const float sq = b[q] * b[q];
+                  ss = ss + sq;
+                }
+              }
+            }
           }
+        }
+      }
+      if constexpr (EPI == WANMI_EPI_BF16) {
+        // the token's sum over the wave's 128 columns: lane h = 0's part, then lane h = 1's
+        if (g.row_sumsq && nw < g.sumsq_cols) {
+          const float other = __shfl_xor(ss, 32, 64);
+          const float tot = h == 0 ? ss + other : other + ss;
+          const int m = m0 + wm * 128 + j * 32 + r32;
+          if (h == 0 && m < (int)g.M) g.row_sumsq[(uint32_t)m * (uint32_t)(g.N / 128) + (uint32_t)(nw / 128)] = tot;
         }
       }
       if constexpr (EPI == WANMI_EPI_GELU_MX) {
@@ -577,13 +601,11 @@ static void launch_gemm(int epilogue, dim3 grid, hipStream_t stream, const GemmA
 
 }  // namespace wanmi
 
-extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
-                                const uint8_t* w_scales, const float* row_scale, const float* col_scale,
-                                const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda,
-                                int epilogue, void* out, int64_t ldo, uint8_t* out_scales,
-                                const void* residual, const float* gate, void* stream) {
-  using namespace wanmi;
-  clear_error();
+namespace wanmi {
+static int gemm_impl(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes, const uint8_t* w_scales,
+                     const float* row_scale, const float* col_scale, const float* bias, int64_t M, int64_t N,
+                     int64_t K, int64_t lda, int epilogue, void* out, int64_t ldo, uint8_t* out_scales,
+                     const void* residual, const float* gate, float* row_sumsq, int64_t sumsq_cols, void* stream) {
   WANMI_REQUIRE(M >= 0 && N > 0 && K > 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: bad sizes M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
   WANMI_REQUIRE(N % TN == 0, WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: N=%lld must be a multiple of %d",
@@ -631,6 +653,8 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   g.gate = epilogue == WANMI_EPI_GATED_RESIDUAL ? gate : nullptr;
   g.out = out;
   g.out_scales = out_scales;
+  g.row_sumsq = row_sumsq;
+  g.sumsq_cols = row_sumsq ? sumsq_cols : 0;
   g.M = M;
   g.N = N;
   g.K = K;
@@ -647,4 +671,29 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
   else
     launch_gemm<false>(epilogue, grid, (hipStream_t)stream, g);
   return check_launch("wanmi_mxfp8_gemm");
+}
+}  // namespace wanmi
+
+extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                                const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                                const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                int epilogue, void* out, int64_t ldo, uint8_t* out_scales,
+                                const void* residual, const float* gate, void* stream) {
+  wanmi::clear_error();
+  return wanmi::gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, N, K, lda, epilogue,
+                          out, ldo, out_scales, residual, gate, nullptr, 0, stream);
+}
+
+extern "C" int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                                         const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                                         const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, void* out,
+                                         int64_t ldo, float* row_sumsq, int64_t sumsq_cols, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(row_sumsq && ((uintptr_t)row_sumsq % 4) == 0, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_rowsumsq: row_sumsq must be a 4-byte aligned pointer");
+  WANMI_REQUIRE(sumsq_cols >= 0 && sumsq_cols <= N && sumsq_cols % 128 == 0, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_rowsumsq: sumsq_cols=%lld must be a multiple of 128 in [0, N]", (long long)sumsq_cols);
+  return gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, N, K, lda, WANMI_EPI_BF16, out,
+                   ldo, nullptr, nullptr, nullptr, row_sumsq, sumsq_cols, stream);
 }

@@ -95,12 +95,17 @@ def mxfp8_linear(
     residual: torch.Tensor | None = None,
     gate: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    row_sumsq: torch.Tensor | None = None,
+    sumsq_cols: int = 0,
 ):
     """``epilogue(x @ W^T * row_scale * col_scale + bias)`` on the MXFP8 GEMM kernel.
 
     ``x``: :class:`MXTensor` ``[..., K]`` or ROW-packed ``[..., K + 4]``. Returns bf16 ``[..., N]``,
     or an :class:`MXTensor` for ``epilogue="gelu_mx"``. ``gated_residual`` computes
     ``bf16(residual + bf16(y) * gate)`` with ``residual`` bf16 ``[..., N]`` and ``gate`` fp32 ``[N]``.
+    ``row_sumsq`` (bf16 epilogue only): fp32 ``[M, N/128]`` receiving, for the column blocks of
+    ``[0, sumsq_cols)``, each row's sum of squares of the bf16 outputs of the block (the input of the
+    across-heads RMSNorm fused into the attention's Q load).
     """
     if epilogue not in EPILOGUES:
         raise ValueError(f"unknown epilogue {epilogue!r}")
@@ -124,6 +129,19 @@ def mxfp8_linear(
             raise ValueError("gated_residual needs residual and gate")
         res2 = residual.reshape(M, N).contiguous()
         gate = gate.reshape(N).to(torch.float32).contiguous()
+    if row_sumsq is not None:
+        if epilogue != "bf16":
+            raise ValueError("row_sumsq needs the bf16 epilogue")
+        _lib.require_gpu(row_sumsq, what="mxfp8_linear")
+        if row_sumsq.shape != (M, N // 128) or row_sumsq.dtype != torch.float32 or not row_sumsq.is_contiguous():
+            raise ValueError(f"row_sumsq must be contiguous fp32 [{M}, {N // 128}]")
+        status = lib.wanmi_mxfp8_gemm_rowsumsq(
+            _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(weight.codes), _lib.ptr(weight.scales), _lib.ptr(row_scale),
+            _lib.ptr(weight.col_scale), _lib.ptr(weight.bias), M, N, K, codes.stride(0), _lib.ptr(out), out.stride(0),
+            _lib.ptr(row_sumsq), int(sumsq_cols), _lib.stream_of(codes),
+        )
+        _lib.check(status, "wanmi_mxfp8_gemm_rowsumsq")
+        return out.reshape(*lead, N)
     status = lib.wanmi_mxfp8_gemm(
         _lib.ptr(codes),
         _lib.ptr(scales),
