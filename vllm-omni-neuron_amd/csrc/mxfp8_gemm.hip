@@ -18,15 +18,18 @@
 // stage buffers filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds, no VGPR round
 // trip), with a 16-byte-chunk XOR swizzle (chunk ^ (row & 7)) so the MFMA operand reads of eight
 // consecutive rows land on distinct banks. Each stage's loads are issued two stages ahead into the
-// buffer just consumed; operands are read per 64-deep slice into ping-pong registers so LDS reads
-// overlap the previous slice's MFMAs. Block scales travel four stages at a time (16 bytes per row
-// in one load, double-buffered): a row's scale bytes are 4 bytes per stage, so per-stage loads
-// would cost an address-unit pass over 64 scattered rows for every 4 bytes.
+// buffer just consumed; operands are read per 64-deep slice into ping-pong registers, interleaved
+// with the MFMAs of the other slice, and a stage needs one barrier. Block scales travel four stages
+// at a time (16 bytes per row in one load, double-buffered): a row's scale bytes are 4 bytes per
+// stage, so per-stage loads would cost an address-unit pass over 64 scattered rows for every 4 bytes.
 //
 // Measured on MI355X, these choices matter: direct-to-LDS loads with a non-zero scalar offset run
-// ~45% slower than with the whole offset in the VGPR, so row-group offsets live in VGPRs; and the
-// loads are issued from inline asm, invisible to the compiler's wait-count pass, which would
-// otherwise put a full vmcnt(0) before every LDS read and serialize the pipeline.
+// ~45% slower than with the whole offset in the VGPR, so the offsets are VGPR sums of a per-lane part
+// held through the k loop and a wave-uniform part; the loads are issued from inline asm, invisible
+// to the compiler's wait-count pass, which would otherwise put a full vmcnt(0) before every LDS read
+// and serialize the pipeline; and the k loop's order of reads, loads and MFMAs is pinned with
+// scheduling barriers (10% faster than the compiler's own order, which moved MFMAs across the
+// stage barriers and left the reads of a slice exposed).
 //
 // The kernel is persistent: one workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ... in an
 // order where each XCD (workgroup ids are dealt round-robin over 8 XCDs) owns a contiguous,
@@ -53,7 +56,6 @@ constexpr int kScaleGroup = 4;                    // stages per scale load (16 b
 constexpr int kVecFloats = 4 * 256;  // per tile: bias[n], col_scale[n], gate[n], row_scale[m]
 constexpr int kGroupM = 8;
 constexpr int kCodeLoads = 16;   // direct-to-LDS loads per wave per stage of codes (16 x 1 KiB)
-constexpr int kScaleLoads = 2;   // per wave per scale group (W rows, A rows; 16 B per row)
 
 struct GemmArgs {
   const uint8_t* a;         // [M, lda]
@@ -98,23 +100,29 @@ struct SliceOperands {
   int as[4];
 };
 
-// Reads slice s (0 or 1) of an LDS stage. Lane data: bytes 0-15 = k[64s + 16h, +16),
-// bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of its row, in word q
-// (the stage's position in its scale group) of the row's 16 scale bytes in `sc` ([2][256] x 16 B:
-// W rows, then A rows).
+// Per-lane offset of a lane's scale bytes in a scale buffer: row (lane & 31) of its 32-row fragment,
+// 16 bytes per row, plus h = lane >> 5 (the lane's 32-block of the slice). Computed once per tile and
+// held through the k loop, so a slice's scale reads cost no address arithmetic.
+__device__ __forceinline__ uint32_t scale_lane_offset() {
+  const uint32_t l = (uint32_t)fresh_lane_id();
+  return (l & 31) * 16 + (l >> 5);
+}
+
+// Reads fragments [I0, I1) of slice s (0 or 1) of an LDS stage. Lane data: bytes 0-15 =
+// k[64s + 16h, +16), bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of
+// its row, byte 4q + 2s + h (q = the stage's position in its scale group) of the row's 16 scale bytes
+// in `sc` ([2][256] x 16 B: W rows, then A rows), read as a byte so the MFMA takes it as is.
+template <int I0 = 0, int I1 = 4>
 __device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& op,
-                                           int wn, int wm, int h, int r32) {
+                                           int wn, int wm, int h, int r32, uint32_t sl) {
   const uint8_t* sw = base;
   const uint8_t* sa = base + TN * BK;
   const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
-  const int sh = 8 * (2 * s + h);
-  // scale-word addresses from a freshly computed lane id: held across the loop they would be one
-  // more set of long-lived VGPRs per scale buffer and word, which the allocator spills
-  const int fr = fresh_lane_id() & 31;
-  const uint32_t* scw = sc + (wn * 128 + fr) * 4 + q;
-  const uint32_t* sca = sc + (TN + wm * 128 + fr) * 4 + q;
+  const uint8_t* scb = reinterpret_cast<const uint8_t*>(sc) + 4 * q + 2 * s;
+  const uint8_t* scw = scb + wn * 128 * 16 + sl;
+  const uint8_t* sca = scb + (TN + wm * 128) * 16 + sl;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = I0; i < I1; ++i) {
     const int rw = wn * 128 + i * 32 + r32;
     const uint4 x0 = *reinterpret_cast<const uint4*>(sw + swz(rw, c0));
     const uint4 x1 = *reinterpret_cast<const uint4*>(sw + swz(rw, c1));
@@ -123,8 +131,8 @@ __device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* 
     const uint4 y0 = *reinterpret_cast<const uint4*>(sa + swz(ra, c0));
     const uint4 y1 = *reinterpret_cast<const uint4*>(sa + swz(ra, c1));
     op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
-    op.ws[i] = (int)((scw[i * 32 * 4] >> sh) & 0xFFu);
-    op.as[i] = (int)((sca[i * 32 * 4] >> sh) & 0xFFu);
+    op.ws[i] = (int)scw[i * 32 * 16];
+    op.as[i] = (int)sca[i * 32 * 16];
   }
 }
 
@@ -182,42 +190,72 @@ __device__ __forceinline__ u32x4 maybe_empty(u32x4 r, bool valid) {
 // 64w .. 64w+63 of each operand tile, 8 rows (1 KiB) per instruction: in row group p (rows
 // 64w + 8p + (l >> 3)) lane l lands in physical 16-byte slot l & 7 and fetches the logical chunk
 // (l & 7) ^ f(row) = (l & 7) ^ (l >> 3) ^ (p & 1). The loads go in pairs (row group p of W and of
-// the activations) so they can be spread between MFMAs. Lane offsets are recomputed per pair from
-// the lane id (holding them across the MFMA block would spill operands), with one full-rate 24-bit
-// multiply-add per load (rows < 256; K and lda < 2^24, checked on the host) in place of a 64-bit
-// one. Token rows past M fall outside the activations' descriptor extent and read as zero.
-__device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
-                                              int p, bool valid = true) {
+// the activations). A lane's offset splits into a per-lane part, row l >> 3 times the row stride
+// plus its chunk (one value for even and one for odd row groups), and a wave-uniform part, the row
+// group and the stage; the k loop holds the per-lane parts in registers (DmaLanes, computed once per
+// tile), so a load costs one add. 24-bit multiplies suffice: rows < 256, and K and lda stay below
+// 2^23 (checked on the host). Token rows past M fall outside the activations' descriptor extent and
+// read as zero.
+struct DmaLanes {
+  uint32_t we, wo, ae, ao;  // W / activations, even / odd row groups
+};
+
+__device__ __forceinline__ DmaLanes dma_lanes(const GemmArgs& g) {
   const uint32_t l = (uint32_t)fresh_lane_id();
   const uint32_t srow = l >> 3;
-  const uint32_t col = ((l & 7) ^ srow ^ (uint32_t)(p & 1)) << 4;
-  const uint32_t kofs = (uint32_t)kt * BK;
+  const uint32_t ce = ((l & 7) ^ srow) << 4, co = ce ^ 16u;
+  const uint32_t rw = (uint32_t)__umul24(srow, (uint32_t)g.K), ra = (uint32_t)__umul24(srow, (uint32_t)g.lda);
+  return DmaLanes{rw + ce, rw + co, ra + ce, ra + co};
+}
+
+__device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, const DmaLanes& dl, int kt,
+                                              uint8_t* buf, int wave, int p, bool valid = true) {
   const uint32_t rg = (uint32_t)(wave * 64 + p * 8);  // first row of the row group
+  const uint32_t kofs = (uint32_t)kt * BK;
   const uint32_t lds = lds_addr(buf) + rg * BK;
-  const uint32_t row = srow + rg;
-  lds_dma_b128(maybe_empty(t.w, valid), (uint32_t)__umul24(row, (uint32_t)g.K) + col + kofs, lds);
-  lds_dma_b128(maybe_empty(t.a, valid), (uint32_t)__umul24(row, (uint32_t)g.lda) + col + kofs, lds + TN * BK);
+  const uint32_t sw = rg * (uint32_t)g.K + kofs, sa = rg * (uint32_t)g.lda + kofs;
+  lds_dma_b128(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
+  lds_dma_b128(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
 }
 
 __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
                                             bool valid = true) {
+  const DmaLanes dl = dma_lanes(g);
 #pragma unroll
-  for (int p = 0; p < 8; ++p) code_dma_pair(g, t, kt, buf, wave, p, valid);
+  for (int p = 0; p < 8; ++p) code_dma_pair(g, t, dl, kt, buf, wave, p, valid);
 }
 
-// The 16 MFMAs of one slice with the 16 code loads of a stage spread between them, one pair after
-// every second MFMA. Issued as one block, the loads would hold the wave at the texture unit's input
-// queue (each moves 1 KiB) while its matrix pipe runs dry; spread out, each pair issues while an
-// MFMA executes. The scheduling barriers keep the compiler from regrouping them.
-__device__ __forceinline__ void mfma_all_with_dma(const SliceOperands& op, f32x16 (&acc)[4][4], const GemmArgs& g,
-                                                  const TileLoads& t, int kt, uint8_t* buf, int wave,
-                                                  bool valid) {
+// One stage of the pipelined k loop is two phases of 16 MFMAs, each split into four fragment rows
+// (4 MFMAs each) with the LDS reads of one fragment row of the next slice issued before them:
+//   phase A: MFMAs on slice 0 (cur), reads of slice 1 of the same stage (nxt);
+//   phase B: MFMAs on slice 1, reads of slice 0 of the next stage, and the stage's 16 code loads, one
+//            pair after the first and third MFMA of each row.
+// Spread this way every read and load issues while an MFMA executes; issued as one block, the loads
+// would hold the wave at the texture unit's input queue (each moves 1 KiB) while its matrix pipe runs
+// dry. The scheduling barriers keep the compiler from regrouping them (it otherwise moves MFMAs
+// across the stage's barrier and clusters the reads).
+template <int I>
+__device__ __forceinline__ void phase_a_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
+                                            const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
+                                            int r32, uint32_t sl) {
+  read_slice<I, I + 1>(base, sc, q, s, nxt, wn, wm, h, r32, sl);
+  __builtin_amdgcn_sched_barrier(0);
+  mfma_rows<I, I + 1>(cur, acc);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int I>
+__device__ __forceinline__ void phase_b_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
+                                            const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
+                                            int r32, uint32_t sl, const GemmArgs& g, const TileLoads& t,
+                                            const DmaLanes& dl, int kt, uint8_t* buf, int wave, bool valid) {
+  read_slice<I, I + 1>(base, sc, q, s, nxt, wn, wm, h, r32, sl);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int i = q >> 2, j = q & 3;
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
-                                                                 op.as[j]);
-    if (q & 1) code_dma_pair(g, t, kt, buf, wave, q >> 1, valid);
+  for (int j = 0; j < 4; ++j) {
+    acc[I][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.w[I], cur.a[j], acc[I][j], 0, 0, 0, cur.ws[I], 0,
+                                                                 cur.as[j]);
+    if (j == 0 || j == 2) code_dma_pair(g, t, dl, kt, buf, wave, 2 * I + (j >> 1), valid);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -524,41 +562,50 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
           issue_codes(g, t, kt + 1, nxt, wave);
         }
         SliceOperands op;
-        read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32);
+        const uint32_t sl = scale_lane_offset();
+        read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32, sl);
         mfma_rows<0, 4>(op, acc);
-        read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32);
+        read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32, sl);
         mfma_rows<0, 4>(op, acc);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
     } else {
-      // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], word
-      // s % 4. Per stage: slice 1 is read and a barrier (every wave has read the stage) lets the
-      // loads of stage s+2 go into the same buffer, spread over the 16 slice-0 MFMAs, so they have
-      // one and a half stages to land; the first half of the slice-1 MFMAs follows; a second barrier
-      // (every wave's stage s+1 has landed) lets slice 0 of stage s+1 be read during the second half.
-      // The scales of group g+1 are loaded with stage 4g+4's codes. The body has no branches
-      // (conditional issue makes the register allocator spill operands): in the last iteration the
-      // loads past the end are issued against an empty resource, which moves no data and zero-fills
-      // buffers nobody reads again, and the slice read after the final barrier is dead.
+      // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], bytes
+      // 4 (s % 4) .. +3 of each row. Entering stage S, opA holds slice 0 of S (its reads may still
+      // be in flight). Phase A runs the slice-0 MFMAs while slice 1 of S is read into opB. Then one
+      // barrier, after this wave's reads of S and loads of S+1 are complete, certifies both that
+      // every wave is done reading S's buffer and that all of S+1 has landed. Phase B runs the slice-1
+      // MFMAs while slice 0 of S+1 is read into opA and stage S+2's codes are loaded into S's buffer,
+      // so every load has the rest of phase B and all of phase A of S+1 (16-32 MFMAs) to land. The
+      // scales of group g+1 are loaded with stage 4g+2's codes: their buffer was last read in stage
+      // 4g-1. The body has no branches (conditional issue makes the register allocator spill
+      // operands): in the last iterations the loads past the end are issued against an empty
+      // resource, which moves no data and zero-fills a buffer nobody reads again, and the slice read
+      // in the final phase B is dead.
 #define WANMI_GEMM_STAGE(S, CUR, OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                     \
   do {                                                                                             \
-    read_slice(CUR, SC_CUR, Q_CUR, 1, opB, wn, wm, h, r32);                                        \
+    phase_a_row<0>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<1>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<2>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<3>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
     __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                   \
-    __syncthreads(); /* every wave has read CUR */                                                 \
-    const bool more_ = (S) + 2 < KT;                                                               \
-    if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
-    mfma_all_with_dma(opA, acc, g, t, more_ ? (S) + 2 : 0, CUR, wave, more_);                      \
-    mfma_rows<0, 2>(opB, acc);                                                                     \
-    /* stage S+1 landed: only stage S+2's loads may still be in flight */                         \
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((WITH_SCALES) ? kCodeLoads + kScaleLoads : kCodeLoads));  \
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));                                                     \
     __syncthreads();                                                                               \
-    read_slice(OTH, SC_NXT, Q_NXT, 0, opA, wn, wm, h, r32);                                        \
-    mfma_rows<2, 4>(opB, acc);                                                                     \
+    const bool more_ = (S) + 2 < KT;                                                               \
+    const int ktn_ = more_ ? (S) + 2 : 0;                                                          \
+    if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
+    phase_b_row<0>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<1>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<2>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<3>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
   } while (0)
 
+      // per-lane load and scale-read offsets, held through the k loop and dead after it
+      const DmaLanes dl = dma_lanes(g);
+      const uint32_t sl = scale_lane_offset();
       SliceOperands opA, opB;
-      read_slice(smem0, ssc[0], 0, 0, opA, wn, wm, h, r32);
+      read_slice(smem0, ssc[0], 0, 0, opA, wn, wm, h, r32, sl);
       for (int kt = 0; kt < KT; kt += 4) {
         const int sg = (kt / kScaleGroup) & 1;  // this group's scale buffer; the next group's is sg ^ 1
         WANMI_GEMM_STAGE(kt, smem0, smem1, ssc[sg], 0, ssc[sg], 1, false);
