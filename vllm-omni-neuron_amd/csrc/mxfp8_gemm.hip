@@ -307,11 +307,22 @@ __device__ __forceinline__ void init_vectors(const GemmArgs& g, float (*svec)[kV
 // ------------------------------------------------------------------------------------------------
 constexpr int kStageWave = 16384;  // LDS staging bytes per wave
 
-// Output stores are non-temporal: the tile is written once and read by the next kernel long after it
-// would have left L2, and streaming it past L2 keeps the stores from competing with the operand
-// traffic of the tiles still in their main loops (measured: 0.2 ms of 2.7 on the QKV projection).
-__device__ __forceinline__ void store_nt16(void* p, uint4 d) {
-  __builtin_nontemporal_store(u32x4{d.x, d.y, d.z, d.w}, reinterpret_cast<u32x4*>(p));
+// Buffer resource over `rows` rows of `row_bytes` bytes from p (rows clamped to [0, 64] by the
+// caller): the hardware drops stores past the extent and returns zero for loads past it. Offsets stay
+// below 64 rows x row_bytes < 2^31 (ldo < 2^22, checked on the host).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, int rows, uint32_t row_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)((uint32_t)rows * row_bytes), 0x00020000);
+}
+// 16-byte store through such a resource, non-temporal (cache policy 2): the tile is written once
+// and read by the next kernel long after it would have left L2, and streaming it past L2 keeps the
+// stores from competing with the operand traffic of the tiles still in their main loops (measured:
+// 0.2 ms of 2.7 on the QKV projection).
+__device__ __forceinline__ void store_rows_nt16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 d) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{d.x, d.y, d.z, d.w}, r, (int)off, 0, 2);
+}
+__device__ __forceinline__ uint4 load_rows16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // bf16 staging: [64 tokens][256 B], 16-byte chunk index XOR (token & 15) -- the 16 lanes of an LDS
@@ -320,47 +331,67 @@ __device__ __forceinline__ int stg16(int tok, int chunk) { return tok * 256 + ((
 // e4m3 staging: [64 tokens][128 B], chunk XOR ((token >> 1) & 7) (two 128-byte rows per bank cycle).
 __device__ __forceinline__ int stg8(int tok, int chunk) { return tok * 128 + ((chunk ^ ((tok >> 1) & 7)) << 4); }
 
-// Scaled, biased accumulator values of tile (i, j) for this lane: v = (acc * row_scale) * col_scale
-// + bias (absent vectors hold their neutral values, so this is exact without them). `scaled` is
-// false when neither scale vector is given (the MX-only projections): x * 1 == x exactly, so the two
-// multiplies and their LDS reads are skipped with the same result.
-__device__ __forceinline__ void epi_values(const f32x16& a, const float* vec, int nt, int mt, int h, bool scaled,
-                                           float (&v)[16]) {
-#pragma clang fp contract(off)
-  if (!scaled) {
+// The epilogue vectors of a wave's 128 features in registers: lane (h) needs features
+// 32 i + 8 gi + 4 h + q (q = 0..3) of the bias and of the column scales, the same for all 128 tokens,
+// so they are read from LDS once per tile instead of once per 16-value block.
+template <bool kScaled>
+struct EpiVectors {
+  float4 bias[4][4];                      // [i][gi]
+  float4 cs[kScaled ? 4 : 1][kScaled ? 4 : 1];
+};
+
+template <bool kScaled>
+__device__ __forceinline__ void load_epi_vectors(const float* vec, int wn, int h, EpiVectors<kScaled>& ev) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const float4 b = *reinterpret_cast<const float4*>(vec + nt + gi * 8 + h * 4);
-      const float bb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[gi * 4 + q] = a[gi * 4 + q] + bb[q];
+      const int nl = wn * 128 + i * 32 + gi * 8 + h * 4;
+      ev.bias[i][gi] = *reinterpret_cast<const float4*>(vec + nl);
+      if constexpr (kScaled) ev.cs[i][gi] = *reinterpret_cast<const float4*>(vec + 256 + nl);
     }
-    return;
-  }
-  const float rsc = vec[768 + mt];
+}
+
+// Scaled, biased accumulator values of tile (i, j) for this lane: v = (acc * row_scale) * col_scale
+// + bias (absent vectors hold their neutral values, so this is exact without them). Without scale
+// vectors (the MX-only projections) x * 1 == x exactly, so the two multiplies are skipped with the
+// same result.
+template <bool kScaled>
+__device__ __forceinline__ void epi_values(const f32x16& a, const EpiVectors<kScaled>& ev, int i, float rsc,
+                                           float (&v)[16]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi) {
-    const int nl = nt + gi * 8 + h * 4;
-    const float4 b = *reinterpret_cast<const float4*>(vec + nl);
-    const float4 cs = *reinterpret_cast<const float4*>(vec + 256 + nl);
+    const float4 b = ev.bias[i][gi];
     const float bb[4] = {b.x, b.y, b.z, b.w};
-    const float cc[4] = {cs.x, cs.y, cs.z, cs.w};
+    if constexpr (!kScaled) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[gi * 4 + q] = (a[gi * 4 + q] * rsc) * cc[q] + bb[q];
+      for (int q = 0; q < 4; ++q) v[gi * 4 + q] = a[gi * 4 + q] + bb[q];
+    } else {
+      const float4 cs = ev.cs[i][gi];
+      const float cc[4] = {cs.x, cs.y, cs.z, cs.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[gi * 4 + q] = (a[gi * 4 + q] * rsc) * cc[q] + bb[q];
+    }
   }
 }
 
 // One wave's 128 x 128 block: two halves of 64 tokens (accumulator columns j = 2 hf, 2 hf + 1).
 // `stage` is the wave's private LDS staging area; LDS operations of one wave complete in order, so
 // the read-back needs no barrier.
-template <int EPI>
+// kScaled / kSumsq: row or column scales given / the bf16 epilogue's per-row sums of squares
+// requested. They are template parameters so that the epilogue is straight-line code: with runtime
+// flags every 16-value block branched, and the LDS reads of its bias and scales were each waited for
+// on the spot.
+template <int EPI, bool kScaled, bool kSumsq>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec, uint8_t* stage,
                                          int m0, int n0, int wm, int wn) {
 #pragma clang fp contract(off)
   const int lane = fresh_lane_id();
   const int h = lane >> 5, r32 = lane & 31;
   const int nw = n0 + wn * 128;  // first feature of the wave's block
-  const bool scaled = g.row_scale || g.col_scale;
+  EpiVectors<kScaled> ev;
+  load_epi_vectors<kScaled>(vec, wn, h, ev);
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     // ---- lane-local math, results into the staging area ----
@@ -375,7 +406,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v[16];
-        epi_values(acc[i][j], vec, wn * 128 + i * 32, wm * 128 + j * 32 + r32, h, scaled, v);
+        epi_values<kScaled>(acc[i][j], ev, i, kScaled ? vec[768 + wm * 128 + j * 32 + r32] : 1.0f, v);
         if constexpr (EPI == WANMI_EPI_GELU_MX) {
           float y[16];
           int e = 0;
@@ -407,7 +438,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
             const uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
             *reinterpret_cast<uint2*>(stage + stg16(tok, 4 * i + gi) + 8 * h) = make_uint2(p0, p1);
             if constexpr (EPI == WANMI_EPI_BF16) {
-              if (g.row_sumsq) {
+              if constexpr (kSumsq) {
                 const float b[4] = {bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -421,7 +452,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       }
       if constexpr (EPI == WANMI_EPI_BF16) {
         // the token's sum over the wave's 128 columns: lane h = 0's part, then lane h = 1's
-        if (g.row_sumsq && nw < g.sumsq_cols) {
+        if (kSumsq && nw < g.sumsq_cols) {
           const float other = __shfl_xor(ss, 32, 64);
           const float tot = h == 0 ? ss + other : other + ss;
           const int m = m0 + wm * 128 + j * 32 + r32;
@@ -436,29 +467,36 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       }
     }
     // ---- read back whole row segments and store them ----
+    // The half's 64 token rows go through a buffer resource whose extent ends at row M: stores to
+    // rows past it are dropped and residual loads from them read zero, so there is no per-row branch
+    // (with one, the compiler waited for each staging read inside its branch).
     const int mbase = m0 + wm * 128 + hf * 64;
+    const int rows = max(0, min(64, (int)g.M - mbase));
+    // Loads issued before the epilogue (the next tile's stage 0, when prefetched here) must be
+    // complete before the first store: vmcnt counts loads and stores together and stores may finish
+    // out of order with loads, so once stores are queued between them and the next tile's stage-1
+    // loads, the partial vmcnt wait at the top of the tile would no longer certify stage 0.
+    if (hf == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     if constexpr (EPI == WANMI_EPI_GELU_MX) {
-      uint8_t* codes = reinterpret_cast<uint8_t*>(g.out);
+      const uint32_t rb = (uint32_t)g.ldo;  // bytes per output row
+      const auto orsrc = rows_rsrc(reinterpret_cast<uint8_t*>(g.out) + (size_t)mbase * rb + nw, rows, rb);
       const int chunk = lane & 7;
+      uint4 d[8];
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int tok = it * 8 + (lane >> 3);
-        const uint4 d = *reinterpret_cast<const uint4*>(stage + stg8(tok, chunk));
-        const int m = mbase + tok;
-        if (m < (int)g.M) store_nt16(codes + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 16)), d);
-      }
+      for (int it = 0; it < 8; ++it) d[it] = *reinterpret_cast<const uint4*>(stage + stg8(it * 8 + (lane >> 3), chunk));
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        store_rows_nt16(orsrc, (uint32_t)(it * 8 + (lane >> 3)) * rb + (uint32_t)chunk * 16, d[it]);
     } else if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) {
       // out = bf16(res + bf16(v) * gate), 8 features per lane; the residual is read coalesced too
-      uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
+      const uint32_t rb = (uint32_t)g.ldo * 2;
+      const auto rrsrc = rows_rsrc(g.residual + (size_t)mbase * g.ldo + nw, rows, rb);
+      const auto orsrc = rows_rsrc(reinterpret_cast<uint16_t*>(g.out) + (size_t)mbase * g.ldo + nw, rows, rb);
       const int chunk = lane & 15;
       uint4 res[16];
 #pragma unroll
-      for (int it = 0; it < 16; ++it) {
-        const int m = mbase + it * 4 + (lane >> 4);
-        res[it] = m < (int)g.M ? *reinterpret_cast<const uint4*>(g.residual + ((uint32_t)m * (uint32_t)g.ldo +
-                                                                            (uint32_t)(nw + chunk * 8)))
-                               : make_uint4(0, 0, 0, 0);
-      }
+      for (int it = 0; it < 16; ++it)
+        res[it] = load_rows16(rrsrc, (uint32_t)(it * 4 + (lane >> 4)) * rb + (uint32_t)chunk * 16);
       const float4 g0 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8);
       const float4 g1 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8 + 4);
       const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
@@ -475,19 +513,21 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
           const float y1 = bf16_hi(rv[k]) + bf16_hi(dv[k]) * gg[2 * k + 1];
           o[k] = pack_bf16x2(y0, y1);
         }
-        const int m = mbase + tok;
-        if (m < (int)g.M)
-          store_nt16(out + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 8)), make_uint4(o[0], o[1], o[2], o[3]));
+        store_rows_nt16(orsrc, (uint32_t)tok * rb + (uint32_t)chunk * 16, make_uint4(o[0], o[1], o[2], o[3]));
       }
     } else {
-      uint16_t* out = reinterpret_cast<uint16_t*>(g.out);
+      const uint32_t rb = (uint32_t)g.ldo * 2;
+      const auto orsrc = rows_rsrc(reinterpret_cast<uint16_t*>(g.out) + (size_t)mbase * g.ldo + nw, rows, rb);
       const int chunk = lane & 15;
 #pragma unroll
-      for (int it = 0; it < 16; ++it) {
-        const int tok = it * 4 + (lane >> 4);
-        const uint4 d = *reinterpret_cast<const uint4*>(stage + stg16(tok, chunk));
-        const int m = mbase + tok;
-        if (m < (int)g.M) store_nt16(out + ((uint32_t)m * (uint32_t)g.ldo + (uint32_t)(nw + chunk * 8)), d);
+      for (int b = 0; b < 2; ++b) {  // two batches of 8 reads, then 8 stores
+        uint4 d[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it)
+          d[it] = *reinterpret_cast<const uint4*>(stage + stg16((b * 8 + it) * 4 + (lane >> 4), chunk));
+#pragma unroll
+        for (int it = 0; it < 8; ++it)
+          store_rows_nt16(orsrc, (uint32_t)((b * 8 + it) * 4 + (lane >> 4)) * rb + (uint32_t)chunk * 16, d[it]);
       }
     }
   }
@@ -538,7 +578,9 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     // tile state is recomputed per tile (cheap scalar work) rather than carried across the epilogue
     const TileLoads t = tile_loads(g, v);
     // This tile's stage 0, scales and vectors have landed; in the pipelined loop stage 1 (the
-    // youngest 16 loads) may still be in flight.
+    // youngest 16 loads) may still be in flight. The partial wait is exact because loads complete in
+    // order among themselves and the previous epilogue's stores were issued either after a full wait
+    // that retired stage 0 or before stage 0 was issued.
     if constexpr (kPipelined)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCodeLoads));
     else
@@ -625,7 +667,22 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
     if (kPrefetchBeforeEpilogue && has_next) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
-    epilogue<EPI>(g, acc, svec[vb], smem1 + wave * kStageWave, m0, n0, wm, wn);
+    {
+      uint8_t* stage = smem1 + wave * kStageWave;
+      const bool scaled = g.row_scale || g.col_scale;
+      if constexpr (EPI == WANMI_EPI_BF16) {
+        if (g.row_sumsq) {
+          if (scaled) epilogue<EPI, true, true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+          else epilogue<EPI, false, true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+        } else {
+          if (scaled) epilogue<EPI, true, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+          else epilogue<EPI, false, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+        }
+      } else {
+        if (scaled) epilogue<EPI, true, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+        else epilogue<EPI, false, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+      }
+    }
     if (!has_next) break;
     __syncthreads();  // every wave is done with its staging area in smem1
     if (!kPrefetchBeforeEpilogue) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
@@ -687,6 +744,8 @@ static int gemm_impl(const uint8_t* a_codes, const uint8_t* a_scales, const uint
   // multiplies of the load offsets
   WANMI_REQUIRE(TN * K < (1LL << 31) && TM * lda < (1LL << 31), WANMI_ERR_UNSUPPORTED,
                 "wanmi_mxfp8_gemm: K=%lld / lda=%lld too large", (long long)K, (long long)lda);
+  // the epilogue's store resources span 64 output rows with 32-bit offsets
+  WANMI_REQUIRE(ldo < (1LL << 22), WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: ldo=%lld too large", (long long)ldo);
 
   GemmArgs g;
   g.a = a_codes;

@@ -96,22 +96,25 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // every later LDS read wait for all outstanding loads (vmcnt(0)), which serializes a multi-stage
 // pipeline. The caller therefore waits explicitly (s_waitcnt vmcnt(n) for its own loads, then a
 // barrier) before any wave reads the destination.
-// An LDS DMA reads M0 and needs one wait state after an SALU write of M0. The compiler inserts it in
-// front of the intrinsic, but not in front of inline asm, and it writes M0 (the "{m0}" operand)
-// immediately before the asm block, so each block starts with s_nop 0.
+// The compiler's hazard recognizer does not look inside inline asm, so each block starts with the
+// wait states the load may need: an LDS DMA reads M0 and needs one wait state after an SALU write of
+// M0 (the compiler writes the "{m0}" operand immediately before the block), and a vector memory
+// instruction that reads an SGPR written by a VALU instruction (v_readlane / v_readfirstlane, which
+// is how spilled SGPRs such as a resource or soffset are reloaded) needs five. s_nop 4 gives five.
+// (With s_nop 0 a spill reload of the soffset right before the load made it read a stale offset.)
 __device__ __forceinline__ void lds_dma_b128(u32x4 rsrc, uint32_t voff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void lds_dma_b32(u32x4 rsrc, uint32_t voff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 // The same with a wave-uniform byte offset `soff` (an SGPR) added to every lane's `voff`, so that
 // per-stage and per-row-group offsets cost no VGPRs.
 __device__ __forceinline__ void lds_dma_b128(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void lds_dma_b32(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
 }
 
 // Lane index recomputed on the spot (volatile, so not merged with earlier copies): code that runs
