@@ -76,7 +76,8 @@ int wanmi_adaln_quant(const void* hidden, const void* residual, const float* gat
  * row_scale [M], col_scale [N], bias [N], gate [N]: fp32, each optional except as the epilogue
  * needs (row/col scales give the reference's ROW_MX dequant with neutral 127 block scales);
  * out: bf16 or e4m3fn [M, ldo]; out_scales: e8m0 [M, N/32] (GELU_MX); residual: bf16 [M, ldo].
- * Requires N % 256 == 0, K % 128 == 0.
+ * Requires N % 256 == 0, K % 128 == 0, 256 * K and 256 * lda below 2^31, M * ldo below 2^32 and
+ * ldo below 2^22 (32-bit buffer offsets).
  * Replaces the ROW_MX projection kernels behind row_mx_qkv_proj / row_mx_o_proj / row_mx_mlp
  * (vllm_omni_neuron/diffusion/quantization/row_mx_kernels.py:48-198): _qkv_cte_mx_impl
  * (kernels/nkilib/core/qkv/qkv_cte.py:2725) and mlp_cte_mx (kernels/nkilib/core/mlp/mlp_cte/mx/).
