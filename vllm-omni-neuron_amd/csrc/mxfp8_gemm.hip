@@ -34,8 +34,9 @@
 // The kernel is persistent: one workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ... in an
 // order where each XCD (workgroup ids are dealt round-robin over 8 XCDs) owns a contiguous,
 // L2-friendly run of tiles grouped 4 deep along m (measured against 2, 8 and 16: 1-5% faster). The
-// next tile's first two stages and its epilogue vectors (bias, column/row scales, gate; staged in LDS) are loaded while the current
-// tile's epilogue runs, so the epilogue overlaps the next tile's load latency.
+// next tile's first two stages and its epilogue vectors (bias, column/row scales, gate; staged in
+// LDS) are loaded while the current tile's epilogue runs, so the epilogue overlaps the next tile's
+// load latency.
 //
 // Reference semantics: the ROW_MX projection epilogues of _qkv_cte_mx_impl / _dequant_row_mx
 // (vllm_omni_neuron/kernels/nkilib/core/qkv/qkv_cte.py:3711-3750, 3996-4021) and of the MLP
