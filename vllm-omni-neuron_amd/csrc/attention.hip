@@ -374,7 +374,14 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
         if (qok) out[d * a.o_ds] = (uint16_t)(pack_bf16x2(acc_o[dt][r] * inv, 0.0f) & 0xFFFFu);
       }
   } else {  // MX codes, token-major; a 32-wide block of d is one d tile, split between lane and lane^32
-    uint8_t* out = reinterpret_cast<uint8_t*>(a.out) + h * a.o_hs + qi * a.o_ss;
+    // Each wave's 32 query rows (128 code bytes each) are staged in LDS and written as whole rows,
+    // 16 bytes per lane; written straight from the accumulator layout every store instruction would
+    // touch 32 rows with 4 bytes each. The staging slot is that of tile ntiles - 3 (or one never
+    // filled), which no wave reads after the last tile's barrier; 16-byte chunks are XOR-swizzled by
+    // the row so that the writes and the row reads spread over the banks. A query's four scale bytes
+    // (d tiles 0-3) go out as one word.
+    uint8_t* stg = (wave < 4 ? sK[(ntiles + 1) % kStages] : sV[(ntiles + 1) % kStages]) + (wave & 3) * 4096;
+    uint32_t sw = 0;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       float y[16];
@@ -387,13 +394,22 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
       e = max_with_lane_xor32(e);
       const int sx = max(e - 7, 0);
       const float f = mx_inv_scale(sx);
+      sw |= (uint32_t)sx << (8 * dt);
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
         const int d = dt * 32 + gi * 8 + hq * 4;
         const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
-        if (qok) *reinterpret_cast<uint32_t*>(out + d) = c4;
+        *reinterpret_cast<uint32_t*>(stg + col * 128 + ((((d >> 4) ^ (col & 7)) << 4) | (d & 15))) = c4;
       }
-      if (qok && hq == 0) a.out_scales[qi * a.os_ss + h * 4 + dt] = (uint8_t)sx;
+    }
+    if (qok && hq == 0) *reinterpret_cast<uint32_t*>(a.out_scales + qi * a.os_ss + h * 4) = sw;
+    uint8_t* out = reinterpret_cast<uint8_t*>(a.out) + h * a.o_hs;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int qr = it * 8 + (lane >> 3), ch = lane & 7;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + qr * 128 + ((ch ^ (qr & 7)) << 4));
+      const int64_t qg = q0 + qr;
+      if (qg < a.Sq) *reinterpret_cast<uint4*>(out + qg * a.o_ss + ch * 16) = v;
     }
   }
 }
@@ -482,6 +498,11 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
   WANMI_REQUIRE(q && k && vt && kmax && out, WANMI_ERR_ARG, "wanmi_attention_const_max: null pointer");
   WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_MX || out_scales, WANMI_ERR_ARG,
                 "wanmi_attention_const_max: MX output needs out_scales");
+  // MX rows are written 16 bytes at a time and a query's four scale bytes as one word
+  WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_MX ||
+                    (((uintptr_t)out % 16) == 0 && o_head_stride % 16 == 0 && o_token_stride % 16 == 0 &&
+                     ((uintptr_t)out_scales % 4) == 0 && os_token_stride % 4 == 0),
+                WANMI_ERR_ARG, "wanmi_attention_const_max: MX output needs 16-byte aligned rows and 4-byte aligned scales");
   // descriptors cover one wave's 32 queries, one 64-key tile, one head of V^T
   WANMI_REQUIRE((31 * q_token_stride + 128) * 2 < (1LL << 31) && (63 * k_token_stride + 128) * 2 < (1LL << 31) &&
                     128 * vt_ld * 2 < (1LL << 31),
