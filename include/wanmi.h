@@ -138,7 +138,8 @@ int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t token_stride
 #define WANMI_ATTN_OUT_TOKEN 0  /* bf16, element (h, s, d) at out[h*o_head + s*o_token + d] */
 #define WANMI_ATTN_OUT_DMAJOR 1 /* bf16, element (h, s, d) at out[h*o_head + d*o_d + s] ([B,N,D,S]) */
 #define WANMI_ATTN_OUT_MX 2     /* e4m3fn codes at out[h*o_head + s*o_token + d] (bytes) and e8m0
-                                   scales at out_scales[s*os_token + h*4 + d/32] */
+                                   scales at out_scales[s*os_token + h*4 + d/32]; out, o_head and
+                                   o_token multiples of 16, out_scales and os_token multiples of 4 */
 
 /*
  * Non-causal constant-max attention, head_dim 128, bf16 inputs, fp32 accumulation:
