@@ -1,0 +1,56 @@
+"""The build's check of the hot-loop direct-to-LDS loads (CPU).
+
+A vector instruction that writes an SGPR (a spill reload by v_readlane, v_readfirstlane) needs five
+wait states before a vector memory instruction reads that SGPR; the compiler does not check inline
+asm. The hot loads carry one wait state (M0's), so the build scans the generated code and falls back
+to five everywhere if a load could read a freshly written resource or offset.
+"""
+
+import importlib.util
+import pathlib
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+_spec = importlib.util.spec_from_file_location("wanmi_build", ROOT / "vllm-omni-neuron_amd" / "build.py")
+build = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(build)
+
+
+def _asm(*lines):
+    return "\n".join("\t" + ln if not ln.endswith(":") else ln for ln in lines) + "\n"
+
+
+def test_flags_a_spill_reload_feeding_the_offset():
+    asm = _asm("v_readlane_b32 s50, v255, 7", "s_nop 0", "buffer_load_dword v0, s[44:47], s50 offen lds")
+    assert len(build.dma_sgpr_hazards(asm)) == 1
+
+
+def test_flags_a_vector_write_of_the_resource():
+    asm = _asm("v_readfirstlane_b32 s45, v3", "s_mov_b32 m0, s2", "s_nop 0",
+               "buffer_load_dwordx4 v0, s[44:47], 0 offen lds")
+    assert len(build.dma_sgpr_hazards(asm)) == 1
+
+
+def test_five_wait_states_are_enough():
+    asm = _asm("v_readlane_b32 s50, v255, 7", "s_nop 4", "buffer_load_dword v0, s[44:47], s50 offen lds")
+    assert build.dma_sgpr_hazards(asm) == []
+    asm = _asm("v_readlane_b32 s50, v255, 7", "s_mov_b32 s1, s2", "s_mov_b32 s3, s4", "s_mov_b32 s5, s6",
+               "s_mov_b32 m0, s7", "s_nop 0", "buffer_load_dword v0, s[44:47], s50 offen lds")
+    assert build.dma_sgpr_hazards(asm) == []
+
+
+def test_scalar_writes_and_unrelated_vector_work_pass():
+    asm = _asm("s_mov_b32 s44, s1", "v_add_u32_e32 v4, s9, v0", "s_mov_b32 m0, s2", "s_nop 0",
+               "buffer_load_dwordx4 v4, s[44:47], 0 offen lds")
+    assert build.dma_sgpr_hazards(asm) == []
+
+
+def test_block_boundary_inside_the_window_is_a_hazard():
+    asm = _asm(".LBB0_7:", "s_nop 0", "buffer_load_dwordx4 v0, s[44:47], 0 offen lds")
+    assert len(build.dma_sgpr_hazards(asm)) == 1
+    asm = _asm("s_cbranch_scc1 .LBB0_9", "s_nop 0", "buffer_load_dwordx4 v0, s[44:47], 0 offen lds")
+    assert len(build.dma_sgpr_hazards(asm)) == 1
+
+
+def test_ordinary_loads_are_not_checked():
+    asm = _asm("v_readfirstlane_b32 s45, v3", "buffer_load_dwordx4 v[0:3], v1, s[44:47], 0 offen")
+    assert build.dma_sgpr_hazards(asm) == []

@@ -9,6 +9,7 @@ from __future__ import annotations
 import concurrent.futures
 import os
 import pathlib
+import re
 import shutil
 import subprocess
 
@@ -40,12 +41,82 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the gfx950 kernels cannot be built")
 
 
-def _compile(src: pathlib.Path) -> pathlib.Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+_SREG = re.compile(r"\bs\[(\d+):(\d+)\]|\bs(\d+)\b|\b(vcc_lo|vcc_hi|vcc)\b")
+_VCC = {"vcc_lo": {106}, "vcc_hi": {107}, "vcc": {106, 107}}
+
+
+def _sgprs(text: str) -> set[int]:
+    out: set[int] = set()
+    for m in _SREG.finditer(text):
+        if m.group(1):
+            out |= set(range(int(m.group(1)), int(m.group(2)) + 1))
+        elif m.group(3):
+            out.add(int(m.group(3)))
+        else:
+            out |= _VCC[m.group(4)]
+    return out
+
+
+def dma_sgpr_hazards(asm: str, window: int = 5) -> list[str]:
+    """Direct-to-LDS loads of `asm` (gfx950 device assembly) that may read an SGPR a vector
+    instruction wrote fewer than `window` wait states before (the hardware needs five; the compiler
+    does not check inline asm). Conservative: any vector instruction naming one of the load's SGPRs
+    counts, and a label or branch inside the window counts as a hazard."""
+    lines = [ln.split(";")[0].strip() for ln in asm.splitlines()]
+    found = []
+    for i, ln in enumerate(lines):
+        if not ln.startswith("buffer_load") or " lds" not in ln:
+            continue
+        used = _sgprs(ln.split(None, 1)[1])
+        states, j = 0, i - 1
+        while states < window and j >= 0:
+            prev = lines[j]
+            j -= 1
+            if not prev or prev.startswith((".", "#")) and not prev.endswith(":"):
+                continue
+            if prev.endswith(":") or prev.startswith(("s_branch", "s_cbranch", "s_setpc", "s_swappc")):
+                found.append(f"{ln}  (block boundary {window - states} wait states before it)")
+                break
+            op = prev.split()[0]
+            if op == "s_nop":
+                states += int(prev.split()[1], 0) + 1
+                continue
+            if op.startswith("v_") and _sgprs(prev[len(op):]) & used:
+                found.append(f"{ln}  (after {prev})")
+                break
+            states += 1
+    return found
+
+
+def _compile_once(src: pathlib.Path, obj: pathlib.Path, extra: list[str]) -> None:
+    cmd = [_hipcc(), *HIP_FLAGS, *extra, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
+
+
+def _device_asm(src: pathlib.Path, extra: list[str]) -> str:
+    out = BUILD_DIR / (src.stem + ".s")
+    cmd = [_hipcc(), *HIP_FLAGS, *extra, f"-I{INCLUDE_DIR}", "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src.name}:\n{res.stderr}")
+    return out.read_text()
+
+
+def _compile(src: pathlib.Path) -> pathlib.Path:
+    """Compiles one source. A source with hot-loop direct-to-LDS loads (one wait state) is checked
+    in its generated code; if any load may read an SGPR a vector instruction just wrote, the source
+    is rebuilt with WANMI_DMA_ALL_WAITS (five wait states everywhere) and checked again."""
+    obj = BUILD_DIR / (src.stem + ".o")
+    _compile_once(src, obj, [])
+    if "lds_dma_b128_hot" in src.read_text():
+        if dma_sgpr_hazards(_device_asm(src, [])):
+            safe = ["-DWANMI_DMA_ALL_WAITS"]
+            _compile_once(src, obj, safe)
+            left = dma_sgpr_hazards(_device_asm(src, safe))
+            if left:
+                raise RuntimeError(f"{src.name}: direct-to-LDS loads read freshly written SGPRs:\n" + "\n".join(left[:5]))
     return obj
 
 

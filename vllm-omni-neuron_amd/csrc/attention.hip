@@ -189,13 +189,13 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     for (int i = 0; i < 2; ++i) {
       const int key = wave * 8 + i * 4 + k_row;
       const int c = k_pc ^ (key & 15);
-      lds_dma_b128(r_k, (uint32_t)(((key0 + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+      lds_dma_b128_hot(r_k, (uint32_t)(((key0 + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int d = wave * 16 + i * 8 + v_row;
       const int c = v_pc ^ (d & 7) ^ ((d >> 3) & 1);
-      lds_dma_b128(r_v, (uint32_t)((d * a.vt_ld + c * 8) * 2), (uint32_t)(kbase * 2),
+      lds_dma_b128_hot(r_v, (uint32_t)((d * a.vt_ld + c * 8) * 2), (uint32_t)(kbase * 2),
                    lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
     }
   };

@@ -209,14 +209,21 @@ __device__ __forceinline__ DmaLanes dma_lanes(const GemmArgs& g) {
   return DmaLanes{rw + ce, rw + co, ra + ce, ra + co};
 }
 
+// kHot: the k loop's loads (one wait state, checked by the build), else the prologue's (five)
+template <bool kHot = false>
 __device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, const DmaLanes& dl, int kt,
                                               uint8_t* buf, int wave, int p, bool valid = true) {
   const uint32_t rg = (uint32_t)(wave * 64 + p * 8);  // first row of the row group
   const uint32_t kofs = (uint32_t)kt * BK;
   const uint32_t lds = lds_addr(buf) + rg * BK;
   const uint32_t sw = rg * (uint32_t)g.K + kofs, sa = rg * (uint32_t)g.lda + kofs;
-  lds_dma_b128(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
-  lds_dma_b128(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
+  if constexpr (kHot) {
+    lds_dma_b128_hot(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
+    lds_dma_b128_hot(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
+  } else {
+    lds_dma_b128(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
+    lds_dma_b128(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
+  }
 }
 
 __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
@@ -256,7 +263,7 @@ __device__ __forceinline__ void phase_b_row(const uint8_t* base, const uint32_t*
   for (int j = 0; j < 4; ++j) {
     acc[I][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.w[I], cur.a[j], acc[I][j], 0, 0, 0, cur.ws[I], 0,
                                                                  cur.as[j]);
-    if (j == 0 || j == 2) code_dma_pair(g, t, dl, kt, buf, wave, 2 * I + (j >> 1), valid);
+    if (j == 0 || j == 2) code_dma_pair<true>(g, t, dl, kt, buf, wave, 2 * I + (j >> 1), valid);
     __builtin_amdgcn_sched_barrier(0);
   }
 }

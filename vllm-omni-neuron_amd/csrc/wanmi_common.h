@@ -116,6 +116,22 @@ __device__ __forceinline__ void lds_dma_b128(u32x4 rsrc, uint32_t voff, uint32_t
 __device__ __forceinline__ void lds_dma_b32(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
   asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
 }
+// The same 16-byte loads for the hot loops (the GEMM's k loop, the attention's K/V tiles), with only
+// the one wait state M0 needs: there the resource and offset SGPRs are written by scalar
+// instructions. The build checks that in the generated code (any vector instruction touching one of
+// a load's SGPRs within five wait states before it) and, if it finds one, rebuilds the file with
+// WANMI_DMA_ALL_WAITS, which gives these loads the full five as well.
+#ifdef WANMI_DMA_ALL_WAITS
+#define WANMI_DMA_HOT_NOP "s_nop 4\n\t"
+#else
+#define WANMI_DMA_HOT_NOP "s_nop 0\n\t"
+#endif
+__device__ __forceinline__ void lds_dma_b128_hot(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile(WANMI_DMA_HOT_NOP "buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma_b128_hot(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile(WANMI_DMA_HOT_NOP "buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+}
 
 // Lane index recomputed on the spot (volatile, so not merged with earlier copies): code that runs
 // after a register-heavy loop derives its lane-dependent addresses from this instead of keeping
