@@ -83,3 +83,37 @@ def test_self_attention_full_shape_every_query(pkg, dev):
     yd = y.double()
     step = (sc * 2.0**-10).repeat_interleave(32, dim=1)
     assert bool(((dq - yd).abs() <= 2.0**-4 * yd.abs() + step).all())
+
+
+def test_cross_attention_full_shape_every_query(pkg, dev):
+    """Cross-attention of the step: 32760 queries over 512 text keys, 40 heads, across-heads
+    RMSNorm on Q and K without RoPE (as for the text context); every query of every head against
+    fp64 attention at the bars above, repeat bit-identical."""
+    ops = pkg.attention_ops
+    scale = D**-0.5
+    Sk = 512
+    gdev = torch.Generator(device=dev).manual_seed(32)
+    q2d = torch.randn(S, N * D, generator=gdev, device=dev).to(torch.bfloat16)
+    kv = torch.randn(Sk, 2 * N * D, generator=gdev, device=dev).to(torch.bfloat16)
+    gamma = 1.0 + 0.1 * torch.randn(N * D, generator=gdev, device=dev)
+    ops.qk_rmsnorm_rope_(q2d, gamma)
+    kmax = ops.qk_rmsnorm_rope_(kv[:, : N * D], gamma, want_max=True)
+    q = q2d.view(S, N, D)
+    k = kv[:, : N * D].view(Sk, N, D)
+    v = kv[:, N * D :].view(Sk, N, D)
+    vt, _ = ops.transpose_heads(v)
+    out = ops.attention_core(q, k, vt, kmax, scale)
+    assert torch.equal(out, ops.attention_core(q, k, vt, kmax, scale))
+    out = out.view(S, N, D)
+    rows = torch.tensor([0, 255, 256, 32759])
+    ref_slice = oa.torch_attend(q[rows, 7].cpu(), k[:, 7].cpu(), v[:, 7].cpu(), scale, dtype=torch.float64)
+    mine = _attend_fp64(q[rows.to(dev), 7], k[:, 7], v[:, 7], scale).cpu()
+    assert (mine - ref_slice).abs().max() <= 1e-6 * ref_slice.abs().max()
+    for h in range(N):
+        ref = _attend_fp64(q[:, h], k[:, h], v[:, h], scale)
+        o = out[:, h].double()
+        err = (o - ref).abs()
+        m = ref.abs().max()
+        cosv = torch.nn.functional.cosine_similarity(o.flatten(), ref.flatten(), dim=0)
+        assert (err.max() / m).item() <= 2e-2 and cosv.item() >= 0.999, (h, (err.max() / m).item(), cosv.item())
+        assert bool((err <= 2.0**-6 * m).all()), h
