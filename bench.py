@@ -94,7 +94,6 @@ def cpu_baseline(S_full, blocks):
     """Reference BF16 eager block on the host CPU at the 1560-token shape; extrapolated to the
     step: projections/FFN/cross-attention linearly in S, self-attention quadratically."""
     from oracle import block as oblock
-    from oracle import rope as orope
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -162,7 +161,6 @@ def main():
               "(no collectives or sharding); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     pkg = __graft_entry__.load_package()
-    from oracle import rope as orope  # RoPE tables are host-side constants (not timed)
 
     dev = torch.device("cuda:0")
     grid = tuple(int(x) for x in args.grid.split(","))
@@ -174,8 +172,7 @@ def main():
     h0 = torch.randn(S, DIM, device=dev, generator=gen).to(torch.bfloat16)
     temb = torch.randn(6, DIM, device=dev, generator=gen)
     ctx = torch.randn(TXT, DIM, device=dev, generator=gen).to(torch.bfloat16)
-    cos, sin = orope.wan_rope(grid)
-    rope = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    rope = pkg.rope_tables(grid, device=dev)  # built once per generation (not timed)
     crosses = [blk.project_cross_kv(w, ctx) for w in blocks]
     torch.cuda.synchronize()
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define WANMI_ABI_VERSION 1
+#define WANMI_ABI_VERSION 2
 
 #define WANMI_OK 0
 #define WANMI_ERR_ARG (-1)         /* bad pointer / size / enum argument */
@@ -53,7 +53,9 @@ const char* wanmi_last_error(void);
  *   out = y (bf16) | MX(y) | ROW(y)
  * hidden, residual, residual_out: bf16 [T,H]; gate, mul, add: fp32 [H].
  * out: bf16 [T,H] (NONE), e4m3fn [T,H] (MX, with scales [T,H/32]) or uint8 [T,H+4] (ROW).
- * Statistics are exact fixed-grid sums in fp64, so results do not depend on the reduction order.
+ * Row statistics are fp32 sums in one fixed order (each of 64 lanes sums its columns 512c + 8l .. 8l+7
+ * of every 512-column chunk c in sequence, then an xor butterfly over the lanes; two-pass mean and
+ * variance; rstd = fp32(1 / sqrt(fp64(var) + eps))), so the bits do not depend on the launch.
  * Requires H % 32 == 0 and H <= 16384.
  * Replaces adaln_quant_kernel (vllm_omni_neuron/kernels/nkilib/experimental/norm/adaln_quant.py:117)
  * as launched by adaln_modulate (vllm_omni_neuron/diffusion/quantization/adaln_kernels.py:87).
@@ -102,19 +104,44 @@ int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, c
                               void* out, int64_t ldo, float* row_sumsq, int64_t sumsq_cols,
                               void* stream);
 
+/* Channel pairs the RoPE rotation of wanmi_qk_rmsnorm_rope acts on, within each head of 128. */
+#define WANMI_ROTATE_INTERLEAVED 0 /* pair i = channels (2i, 2i+1): Wan's apply_rotary_emb_wan */
+#define WANMI_ROTATE_HALVES 1      /* pair i = channels (i, i+64): rotate-half on channels de-interleaved
+                                      per head (the reference's fused QKV kernel layout) */
+
 /*
- * Across-heads RMSNorm + optional interleaved 3D RoPE, in place on a bf16 [S, heads*128] slab
- * (row stride ld elements):  x = bf16(x * rrms * gamma), rrms = 1/sqrt(mean_row(x^2) + eps);
- * then per pair (2i, 2i+1) of each head: (a, b) -> bf16(a cos - b sin), bf16(a sin + b cos) with
- * cos_tab / sin_tab fp32 [S, 64] (one angle per pair; both NULL = no RoPE). gamma: fp32 [heads*128].
+ * Across-heads RMSNorm + optional 3D RoPE, in place on a bf16 [S, heads*128] slab (row stride ld
+ * elements):  x = bf16(x * rrms * gamma), rrms = 1/sqrt(mean_row(x^2) + eps); then per pair (a, b)
+ * of each head (rope_pairs selects which channels pair): (a, b) -> bf16(a cos - b sin),
+ * bf16(a sin + b cos) with cos_tab / sin_tab fp32 [S, 64] (angle i of pair i; both NULL = no RoPE).
+ * gamma: fp32 [heads*128] in the slab's channel order.
  * maxnorm (optional, fp32 [heads]) receives max over tokens of each head's L2 norm of the output.
  * Replaces DistributedRMSNorm + apply_rotary_emb_wan (vllm_omni_neuron/diffusion/models/wan2_2/
  * wan2_2_transformer.py:879-893, diffusion/layers/rope.py:8-34) and the fused across-heads norm +
  * RoPE epilogue of the QKV kernel (kernels/nkilib/core/qkv/qkv_cte.py:3781-3990).
  */
 int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
-                          const float* cos_tab, const float* sin_tab, float eps, float* maxnorm,
-                          void* stream);
+                          const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
+                          float* maxnorm, void* stream);
+
+/* Table layouts of wanmi_rope_tables (per token s, fp32). */
+#define WANMI_ROPE_PAIRS 0       /* [S, head_dim/2]: angle i of pair i (the kernels' own tables) */
+#define WANMI_ROPE_INTERLEAVED 1 /* [S, head_dim]: each angle twice, (c0, c0, c1, c1, ...) -- the
+                                    reference's freqs_cos / freqs_sin [1, S, 1, head_dim] */
+#define WANMI_ROPE_ROTATE_HALF 2 /* [S, head_dim]: cat([base, base]) -- the rotate-half caches */
+
+/*
+ * Wan 3D rotary tables for a latent patch grid (frames, height, width), S = frames*height*width
+ * tokens in raster order: the head's pairs split into time / height / width axes of
+ * head_dim - 2*(2*(head_dim/6)), 2*(head_dim/6), 2*(head_dim/6) channels; pair j of an axis of dim d
+ * at position p has the angle p / theta^(2j/d) (fp64), written as fp32 cos and sin.
+ * frames, height, width <= max_seq_len (the reference's table length). cos_out / sin_out as the
+ * layout says. Replaces WanRotaryPosEmbed (vllm_omni_neuron/diffusion/layers/rope.py:37-114), called
+ * once per forward at diffusion/models/wan2_2/wan2_2_transformer.py:1757; the rotate-half layout is
+ * _rope_rotate_half_caches (diffusion/quantization/row_mx_modules.py:51-76).
+ */
+int wanmi_rope_tables(int64_t frames, int64_t height, int64_t width, int head_dim, int64_t max_seq_len,
+                      double theta, int layout, float* cos_out, float* sin_out, void* stream);
 
 /*
  * V bf16, element (s, h, d) at v[s*ld + h*head_stride + d] (token-major: head_stride = 128;

@@ -14,11 +14,13 @@ Modules and what pins each:
 - ``adaln``: the canonical fused adaLN (fixed-order fp32 row statistics in the kernel's lane
   order). Pinned against ``math.fsum`` sums within the fp32 error bound, the distance to
   ``F.layer_norm`` / the eager restatement, and LayerNorm invariants.
-- ``rope``: Wan 3D RoPE tables and interleaved rotation. Pinned by norm preservation, the
-  rotate-half equivalence and closed-form angles.
+- ``rope``: Wan 3D RoPE tables, interleaved rotation and the across-heads RMSNorm. Pinned by
+  closed-form angles, norm preservation, the rotate-half equivalence, and closed-form norms of rows
+  whose heads differ in scale (fails a per-head norm) or sit near eps (fails a misplaced eps).
 - ``attention``: exact softmax attention and the constant-max form. Pinned by fp64 brute force,
   invariance to the subtracted constant, and the underflow clamp.
-- ``gemm``: MXFP8 dequantized fp64 products, GELU-tanh MLP. Pinned by brute-force loops on tiny
-  shapes and closed-form GELU points.
+- ``gemm``: MXFP8 dequantized fp64 products and GELU-tanh. Pinned by scalar brute-force loops on
+  tiny shapes (codes decoded by torch's own float8 cast; block, row and column scales and bias
+  placement), published values of the GELU tanh approximation, and the transposed weight layout.
 - ``block``: the Wan transformer block composed from the above (MXFP8 path and BF16 eager path).
 """

@@ -33,8 +33,31 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     """fp32/fp64 values -> e4m3fn codes (uint8), round to nearest even.
 
     Values with |x| >= 464 would round past the largest finite code; callers clip to +-448 first
-    (the MX and ROW rules both do), so such inputs are rejected here.
+    (the MX and ROW rules both do), so such inputs are rejected here. Values exactly representable
+    in fp32 take an integer path on the fp32 bits; other fp64 values are rounded from their fp64
+    magnitude directly (no double rounding through fp32).
     """
+    x = np.asarray(x)
+    x32 = x.astype(np.float32)
+    if x.dtype != np.float32 and not np.array_equal(x32.astype(x.dtype), x):
+        return _e4m3_encode_f64(x)
+    u = x32.view(np.uint32)
+    sign = ((u >> 24) & 0x80).astype(np.uint8)
+    mag = u & np.uint32(0x7FFFFFFF)
+    if np.any(mag >= np.float32(464.0).view(np.uint32)):  # also catches inf / nan
+        raise ValueError("e4m3_encode: input outside the finite e4m3fn rounding range")
+    # normal range (|x| >= 2^-6, biased fp32 exponent >= 121): round the 23-bit mantissa to 3 bits,
+    # nearest even; a carry moves into the exponent, and rebiasing 127 -> 7 subtracts 120 << 3
+    rne = (mag + np.uint32(0x7FFFF) + ((mag >> 20) & 1)) >> 20
+    normal = (rne.astype(np.int64) - (120 << 3))
+    # subnormal range (and zero): magnitude in units of 2^-9, nearest even (exact in fp32); 8 is the
+    # smallest normal, which the same integer encodes
+    sub = np.rint(mag.view(np.float32) * np.float32(512.0)).astype(np.int64)
+    code = np.where(mag >= np.uint32(121 << 23), normal, sub)
+    return (code.astype(np.uint8) | sign).astype(np.uint8)
+
+
+def _e4m3_encode_f64(x: np.ndarray) -> np.ndarray:
     x = np.asarray(x, dtype=np.float64)
     sign = np.signbit(x).astype(np.uint8) << 7
     a = np.abs(x)

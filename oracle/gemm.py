@@ -5,6 +5,7 @@ Restates the ROW_MX / MX projection arithmetic of the reference in fp64:
 - ``_mlp_ref_standard`` (vllm_omni_neuron/kernels/nkilib/core/mlp/mlp_torch.py:401-599):
   ``up = (x * in_scale) @ (W_up * w_scale) + b_up``; ``g = GELU_tanh(up)``; ``(codes, s) = MX(g)``
   (mlp_torch.py:252-271, 586-594); ``out = (codes * 2^(s-127)) @ (W_down * w_scale) + b_down``.
+  The MLP is composed from these pieces in ``block.mxfp8_block`` and in the tests.
 - the QKV / o-proj ROW_MX epilogue ``psum * row_scale * col_scale + bias``
   (kernels/nkilib/core/qkv/qkv_cte.py:3996-4021).
 
@@ -56,17 +57,3 @@ def quantize_weight(w_kn: np.ndarray):
     quantized along K from bf16 values, the layout the GEMM consumes."""
     wt = bf16_round(np.ascontiguousarray(np.asarray(w_kn, np.float32).T))
     return mx_mod.mx_quantize(wt)
-
-
-def mlp_mx(a_codes, a_scales, up, down, b_up=None, b_down=None, inter_bf16=None):
-    """MXFP8 GELU-tanh MLP in fp64. ``up`` / ``down`` are ``(codes, scales)`` weights ``[N, K]``.
-
-    Returns ``(out fp64 [M, H], intermediate bf16 values fp32 [M, I], inter codes, inter scales)``.
-    ``inter_bf16`` overrides the intermediate (e.g. the GPU's own bf16 GELU output) so the down
-    projection can be checked in isolation.
-    """
-    up_out = mx_gemm(a_codes, a_scales, *up, bias=b_up)
-    g = bf16_round(gelu_tanh(up_out).numpy().astype(np.float32)) if inter_bf16 is None else inter_bf16
-    ic, isc = mx_mod.mx_quantize(g)
-    out = mx_gemm(ic, isc, *down, bias=b_down)
-    return out, g, ic, isc

@@ -37,8 +37,9 @@ def mx_quantize(y: np.ndarray):
     blocks = y.reshape(*y.shape[:-1], K // MX_BLOCK, MX_BLOCK)
     emax = exp_field(blocks).max(axis=-1)
     s = np.clip(emax - FP8_MAX_EXP, 0, 255)
-    scaled = np.ldexp(blocks.astype(np.float64), (127 - s)[..., None])
-    scaled = np.clip(scaled, -E4M3_MAX, E4M3_MAX)
+    # y * 2^(127 - s) is exact in fp32: a power-of-two scaling whose results stay below 2^8
+    scaled = blocks * np.ldexp(np.float32(1.0), (127 - s)[..., None]).astype(np.float32)
+    scaled = np.clip(scaled, np.float32(-E4M3_MAX), np.float32(E4M3_MAX))
     codes = e4m3_encode(scaled).reshape(y.shape)
     return codes, s.astype(np.uint8)
 

@@ -1,0 +1,133 @@
+"""Every tensor whose pointer reaches the C ABI is checked on the host first (CPU only).
+
+A wrong dtype, shape or layout raises ValueError before anything is launched; a tensor that is
+not on a GPU raises RuntimeError ("no CPU fallback"). These run on CPU tensors, so a check that
+were missing would surface as the device error instead of the ValueError asserted here.
+"""
+
+import pytest
+import torch
+
+N, K, M = 256, 128, 8
+
+
+@pytest.fixture(scope="module")
+def w(pkg):
+    codes = torch.zeros(N, K, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    scales = torch.full((N, K // 32), 127, dtype=torch.uint8)
+    return pkg.MXWeight(codes, scales, None, torch.zeros(N))
+
+
+@pytest.fixture(scope="module")
+def x(pkg):
+    return pkg.MXTensor(torch.zeros(M, K, dtype=torch.uint8).view(torch.float8_e4m3fn),
+                        torch.full((M, K // 32), 127, dtype=torch.uint8))
+
+
+def test_linear_weight_vectors(pkg, w, x):
+    bad = [
+        w._replace(bias=torch.zeros(N, dtype=torch.bfloat16)),  # bias dtype
+        w._replace(bias=torch.zeros(N + 1)),  # bias shape
+        w._replace(col_scale=torch.zeros(2, N)),  # col_scale shape
+        w._replace(scales=torch.zeros(N, K // 16, dtype=torch.uint8)),  # scales shape
+        w._replace(scales=torch.zeros(N, K // 32, dtype=torch.float32)),  # scales dtype
+    ]
+    for wb in bad:
+        with pytest.raises(ValueError):
+            pkg.mxfp8_linear(x, wb)
+
+
+def test_linear_activation_and_epilogue_operands(pkg, w, x):
+    with pytest.raises(ValueError, match="activation scales"):
+        pkg.mxfp8_linear(x._replace(scales=torch.zeros(M, 3, dtype=torch.uint8)), w)
+    with pytest.raises(ValueError, match="residual"):
+        pkg.mxfp8_linear(x, w, epilogue="gated_residual", residual=torch.zeros(M, N), gate=torch.ones(N))
+    with pytest.raises(ValueError, match="gate"):
+        pkg.mxfp8_linear(x, w, epilogue="gated_residual", residual=torch.zeros(M, N, dtype=torch.bfloat16),
+                         gate=torch.ones(N, dtype=torch.float16))
+    with pytest.raises(ValueError, match="out"):
+        pkg.mxfp8_linear(x, w, out=torch.zeros(M, N))
+    with pytest.raises(ValueError, match="row_sumsq"):
+        pkg.mxfp8_linear(x, w, row_sumsq=torch.zeros(M, 3), sumsq_cols=128)
+    with pytest.raises(ValueError, match="ROW-packed"):
+        pkg.mxfp8_linear(torch.zeros(M, K + 4, dtype=torch.bfloat16), w)
+    # well-formed but on the host: the device check fires
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.mxfp8_linear(x, w)
+
+
+def test_qk_norm_rope_tables(pkg):
+    ops = pkg.attention_ops
+    S, W = 16, 512
+    xq = torch.zeros(S, W, dtype=torch.bfloat16)
+    g = torch.ones(W)
+    ok = torch.zeros(S, 64)
+    for cos, sin in [
+        (ok.to(torch.bfloat16), ok),  # half-width dtype would read past the table
+        (torch.zeros(1, S, 1, 128), torch.zeros(1, S, 1, 128)),  # the reference's interleaved [1,S,1,128]
+        (torch.zeros(S + 1, 64), torch.zeros(S + 1, 64)),  # wrong S
+        (ok.t().contiguous().t(), ok),  # not contiguous
+        (ok, None),
+    ]:
+        with pytest.raises(ValueError):
+            ops.qk_rmsnorm_rope_(xq, g, cos=cos, sin=sin)
+    with pytest.raises(ValueError):
+        ops.qk_rmsnorm_rope_(xq, torch.ones(W - 1))
+    with pytest.raises(ValueError):
+        ops.qk_rmsnorm_rope_(xq, g, rope_pairs="bogus")
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ops.qk_rmsnorm_rope_(xq, g, cos=ok, sin=ok)
+
+
+def test_attention_operands(pkg):
+    ops = pkg.attention_ops
+    Sq, Sk, Nh = 32, 64, 4
+    q = torch.zeros(Sq, Nh, 128, dtype=torch.bfloat16)
+    k = torch.zeros(Sk, Nh, 128, dtype=torch.bfloat16)
+    vt = torch.zeros(Nh, 128, 64, dtype=torch.bfloat16)
+    km = torch.ones(Nh)
+    with pytest.raises(ValueError, match="vt"):
+        ops.attention_core(q, k, vt[:, :, :32], km, 0.1)
+    with pytest.raises(ValueError, match="kmax"):
+        ops.attention_core(q, k, vt, km.double(), 0.1)
+    qp = ops.QPrep(torch.zeros(Sq, Nh), torch.ones(Nh * 128), torch.zeros(Sq, 64, dtype=torch.bfloat16),
+                   torch.zeros(Sq, 64))
+    with pytest.raises(ValueError, match="cos"):
+        ops.attention_core(q, k, vt, km, 0.1, q_prep=qp)
+    with pytest.raises(ValueError, match="sumsq"):
+        ops.attention_core(q, k, vt, km, 0.1, q_prep=ops.QPrep(torch.zeros(Sq, Nh - 1), torch.ones(Nh * 128)))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ops.attention_core(q, k, vt, km, 0.1)
+
+
+def test_drop_in_argument_checks(pkg, w):
+    ops, ct = pkg.attention_ops, pkg.common_types
+    packed = torch.zeros(1, M, K + 4, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="output channels"):
+        ops.row_mx_qkv_proj(packed, w, num_heads=4, head_dim=128, num_kv_heads=4)
+    with pytest.raises(NotImplementedError):
+        ops.row_mx_qkv_proj(packed, w, num_heads=2, head_dim=64, num_kv_heads=0)
+    with pytest.raises(NotImplementedError, match="across-heads"):  # RoPE needs the K norm too
+        cfg = ct.QKNormConfig(q_norm=ct.NormType.RMS_NORM_ACROSS_HEADS, k_norm=None)
+        wk = pkg.MXWeight(torch.zeros(3 * 512, K, dtype=torch.uint8).view(torch.float8_e4m3fn),
+                          torch.full((3 * 512, K // 32), 127, dtype=torch.uint8))
+        ops.row_mx_qkv_proj(packed, wk, num_heads=4, head_dim=128, num_kv_heads=4, fused_rope=True,
+                            qk_norm_pre_rope=cfg, qk_norm_pre_rope_q_gamma=torch.ones(512))
+    with pytest.raises(NotImplementedError):
+        ops.row_mx_qkv_proj(packed, w, num_heads=2, head_dim=128, replica_groups=[[0, 1]])
+    with pytest.raises(ValueError, match="weight scale"):
+        pkg.row_mx_mlp(packed, w, w, up_w_scale=torch.ones(N + 1))
+    with pytest.raises(ValueError, match="K/4, N, 4"):
+        pkg.packed_weight_to_mx(torch.zeros(K, N, dtype=torch.uint8).view(torch.float8_e4m3fn))
+
+
+def test_packed_reference_weight_layout(pkg):
+    """[K/4, N, 4] with four consecutive contraction values innermost -> codes [N, K]."""
+    K4, Nn = 16, 256
+    phys = torch.arange(K4 * Nn * 4, dtype=torch.int64).remainder(251).to(torch.uint8).view(K4, Nn, 4)
+    mw = pkg.packed_weight_to_mx(phys.view(torch.float8_e4m3fn), torch.full((1, Nn), 0.5))
+    codes = mw.codes.view(torch.uint8)
+    for n, k in [(0, 0), (3, 5), (255, 63), (17, 30)]:
+        assert int(codes[n, k]) == int(phys[k // 4, n, k % 4])
+    assert mw.rope_pairs == "halves" and bool((mw.scales == 127).all())
+    assert mw.col_scale.shape == (Nn,) and float(mw.col_scale[7]) == 0.5

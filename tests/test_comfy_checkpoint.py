@@ -99,10 +99,10 @@ def test_validate(ck, ckpt2):
     h = _header(t)
     ck.validate_fp8_checkpoint(h, num_layers=2)
     cases = [
-        ("blocks.1.ffn.0.weight", {"dtype": "BF16"}, "must be F8_E4M3"),
-        ("blocks.0.cross_attn.o.weight", {"shape": [256, 256, 1]}, "must be 2-D"),
-        ("blocks.0.self_attn.k.scale_weight", {"shape": [256]}, "must be scalar"),
-        ("text_embedding.2.scale_weight", {"dtype": "F16"}, "must be F32"),
+        ("blocks.1.ffn.0.weight", {"dtype": "BF16"}, "blocks.1.ffn.0.weight: stored as BF16, the format requires F8_E4M3"),
+        ("blocks.0.cross_attn.o.weight", {"shape": [256, 256, 1]}, "cross_attn.o.weight: shape .* is not a 2-D"),
+        ("blocks.0.self_attn.k.scale_weight", {"shape": [256]}, "self_attn.k.scale_weight: shape .* not a single scalar"),
+        ("text_embedding.2.scale_weight", {"dtype": "F16"}, "stored as F16, the format requires F32"),
     ]
     for key, patch, msg in cases:
         bad = copy.deepcopy(h)
@@ -114,9 +114,10 @@ def test_validate(ck, ckpt2):
         del bad[key]
         with pytest.raises(ck.Fp8CheckpointError, match="missing"):
             ck.validate_fp8_checkpoint(bad, num_layers=2)
-    # a reduced-layer file validates against its own layer count only
-    with pytest.raises(ck.Fp8CheckpointError, match="missing"):
+    # a reduced-layer file validates against its own layer count only; every problem is listed
+    with pytest.raises(ck.Fp8CheckpointError, match="blocks.2.self_attn.q.weight: missing") as exc:
         ck.validate_fp8_checkpoint(h, num_layers=3)
+    assert "20 problems" in str(exc.value)  # 10 checkpoint linears x 2 leaves of block 2, 8 shown
 
 
 def test_host_block_layout_is_exact(ck, ckpt2):

@@ -117,3 +117,70 @@ def test_cross_attention_full_shape_every_query(pkg, dev):
         cosv = torch.nn.functional.cosine_similarity(o.flatten(), ref.flatten(), dim=0)
         assert (err.max() / m).item() <= 2e-2 and cosv.item() >= 0.999, (h, (err.max() / m).item(), cosv.item())
         assert bool((err <= 2.0**-6 * m).all()), h
+
+
+def _projected_q(pkg, dev, seed):
+    """Raw Q as the block makes it: the MXFP8 GEMM of an MX activation, with the per-128-column
+    sums of squares of its bf16 outputs written by the GEMM's epilogue."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randn(S, N * D, generator=g, device=dev).to(torch.bfloat16)
+    aq = pkg.adaln_modulate(a, eps=1e-6, quant="mx")
+    w = (torch.randn(N * D, N * D, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wq = pkg.quantize_weight_mx(w, 0.1 * torch.randn(N * D, generator=g, device=dev))
+    ss = torch.empty(S, N * D // 128, dtype=torch.float32, device=dev)
+    q = pkg.mxfp8_linear(aq, wq, row_sumsq=ss, sumsq_cols=N * D)
+    gamma = 1.0 + 0.1 * torch.randn(N * D, generator=g, device=dev)
+    return q, ss, gamma
+
+
+def _check_heads(out, q_ref, k, v, scale):
+    for h in range(N):
+        ref = _attend_fp64(q_ref[:, h], k[:, h], v[:, h], scale)
+        o = out[:, h].double()
+        err = (o - ref).abs()
+        m = ref.abs().max()
+        cosv = torch.nn.functional.cosine_similarity(o.flatten(), ref.flatten(), dim=0)
+        assert (err.max() / m).item() <= 2e-2 and cosv.item() >= 0.999, (h, (err.max() / m).item(), cosv.item())
+        assert bool((err <= 2.0**-6 * m).all()), h
+
+
+@pytest.mark.parametrize("kind", ["self", "cross"])
+def test_fused_q_prep_attention_full_shape(pkg, dev, kind):
+    """The attention the block and the bench run: Q is the raw projection, normalized across heads
+    from the GEMM's partial sums (and, for self-attention, rotated with the 21x30x52 tables built by
+    the package) as the kernel loads it. Every query of all 40 heads against fp64 attention over
+    the oracle's prepared Q (``DistributedRMSNorm`` + ``apply_rotary_emb_wan`` on the same raw q),
+    at the bars above; repeat launches bit-identical, MX output within e4m3 rounding."""
+    ops = pkg.attention_ops
+    scale = D**-0.5
+    q_raw, ss, gamma = _projected_q(pkg, dev, 41 if kind == "self" else 42)
+    gdev = torch.Generator(device=dev).manual_seed(43)
+    Sk = S if kind == "self" else 512
+    kv = torch.randn(Sk, 2 * N * D, generator=gdev, device=dev).to(torch.bfloat16)
+    gk = 1.0 + 0.1 * torch.randn(N * D, generator=gdev, device=dev)
+    cos = sin = None
+    if kind == "self":
+        cos, sin = pkg.rope_tables((21, 30, 52), device=dev)
+    kmax = ops.qk_rmsnorm_rope_(kv[:, : N * D], gk, cos=cos if kind == "self" else None,
+                                sin=sin if kind == "self" else None, want_max=True)
+    k = kv[:, : N * D].view(Sk, N, D)
+    v = kv[:, N * D :].view(Sk, N, D)
+    vt, _ = ops.transpose_heads(v)
+    qp = ops.QPrep(ss, gamma, cos, sin, 1e-6)
+    q = q_raw.view(S, N, D)
+    out = ops.attention_core(q, k, vt, kmax, scale, q_prep=qp)
+    assert torch.equal(out, ops.attention_core(q, k, vt, kmax, scale, q_prep=qp))
+    mx = ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX, q_prep=qp)
+    # the oracle's Q preparation of the same raw projection
+    qn = orope.rms_norm_across_heads(q_raw.cpu(), gamma.cpu()).view(1, S, N, D)
+    if kind == "self":
+        ic, isn = orope.wan_rope((21, 30, 52))
+        qn = orope.apply_rotary_emb_wan(qn, ic[None, :, None], isn[None, :, None])
+    q_ref = qn[0].to(dev)
+    out = out.view(S, N, D)
+    _check_heads(out, q_ref, k, v, scale)
+    y = out.reshape(S, N * D).double()
+    sc = torch.exp2(mx.scales.double() - 127.0)
+    dq = (mx.codes.view(torch.float8_e4m3fn).double().view(S, -1, 32) * sc.unsqueeze(-1)).view(S, N * D)
+    step = (sc * 2.0**-10).repeat_interleave(32, dim=1)
+    assert bool(((dq - y).abs() <= 2.0**-4 * y.abs() + step).all())

@@ -11,8 +11,10 @@ Two levels of checking:
    inputs to that stage. adaLN stages (codes, scales, bf16 residual) must be bit-exact; bf16 stage
    outputs (GEMMs, norm/RoPE) must meet max|err|/max|ref| <= 2e-2 and cosine >= 0.999; MX stage
    outputs (attention, GELU) are compared with the oracle's MX quantization of its own bf16 result:
-   >= 90% of codes identical (bf16 P moves peaked cross-attention outputs across e4m3 boundaries
-   more often), every element within one e4m3 step plus 2^-7 of its 32-block max, cosine >= 0.999.
+   at least 98% (self-attention), 90% (cross-attention over 512 keys) and 99.5% (GELU) of the codes
+   identical (measured: 99.3%, 92.5%, 99.9%; the attention's bf16 rounding of its pre-scaled Q and
+   of P moves outputs across e4m3 boundaries, most often over the short text sequence), every
+   element within one e4m3 step plus 2^-7 of its 32-block max, cosine >= 0.999.
 2. end to end: the oracle's MXFP8 block from the same block inputs vs the GPU block output:
    cosine >= 0.999, relative RMS error <= 3e-2 and max|err|/max|ref| <= 6e-2. These are set by the
    block's own sensitivity, measured on the oracle alone: moving 0.1% of the input elements by one
@@ -58,7 +60,7 @@ def _close_e2e(got, ref, what):
     assert cos >= 0.999 and rms <= 3e-2 and rel <= 6e-2, (what, rel, rms, cos)
 
 
-def _mx_close(got_mx, ref_bf16, what):
+def _mx_close(got_mx, ref_bf16, what, min_same):
     """GPU MX output vs MX(oracle bf16 output): codes mostly identical; every element within one
     e4m3 step of itself plus 2^-7 of its 32-block's max (bf16-level absolute error of the stage)."""
     rc, rs = omx.mx_quantize(ref_bf16.float().numpy())
@@ -71,7 +73,7 @@ def _mx_close(got_mx, ref_bf16, what):
     worst = float((np.abs(g - r) / tol).max())
     cos = float(np.dot(g.ravel(), r.ravel()) / (np.linalg.norm(g) * np.linalg.norm(r)))
     print(f"{what}: identical codes {same:.4f}, max |diff|/tol {worst:.2f}, cos {cos:.6f}")
-    if not (same >= 0.90 and worst <= 1.0 and cos >= 0.999):
+    if not (same >= min_same and worst <= 1.0 and cos >= 0.999):
         FAILS.append((what, same, worst, cos))
 
 
@@ -98,7 +100,7 @@ def run(pkg, dev):
     temb = torch.randn(6, 5120, generator=gc)
     ctx = torch.randn(512, 5120, generator=gc).to(torch.bfloat16)
     cos, sin = orope.wan_rope(GRID)
-    rope = pkg.attention_ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    rope = pkg.rope_tables(GRID, device=dev)
     cross = blk.project_cross_kv(w, ctx.to(dev))
     snap, live = {}, {}
 
@@ -147,7 +149,7 @@ def test_block_stagewise(pkg, dev, run):
     k, v = (qkv_post[:, i * dim : (i + 1) * dim].view(S, heads, D) for i in (1, 2))
     o1 = snap["self_attention"][0]
     _mx_close(o1, oblock._attend(refn["norm_q"].to(torch.bfloat16).view(S, heads, D), k, v, s),
-              "self-attention with Q RMSNorm+RoPE on load (MX out)")
+              "self-attention with Q RMSNorm+RoPE on load (MX out)", 0.98)
     # o-proj with the gated residual in its epilogue, from the GPU's MX attention output:
     # h1 = bf16(h + bf16(o1 @ Wo + b) * gate)
     h1 = snap["gemm_o"][0].cpu()
@@ -184,7 +186,7 @@ def test_block_stagewise(pkg, dev, run):
     _close(v_gpu.reshape(512, dim), v2, "cross V (projected once)")
     # cross-attention from the GPU's q2 and cached K/V
     o2 = snap["cross_attention"][0]
-    _mx_close(o2, oblock._attend(q2.view(S, heads, D), r["cross"].k.cpu(), v_gpu, s), "cross-attention (MX out)")
+    _mx_close(o2, oblock._attend(q2.view(S, heads, D), r["cross"].k.cpu(), v_gpu, s), "cross-attention (MX out)", 0.90)
     # cross o-proj with the residual in its epilogue: h2 = bf16(h1 + bf16(o2 @ Wo2 + b))
     h2 = snap["gemm_o2"][0].cpu()
     attn2_ref = oblock._lin(*_mx_np(o2), wq["o2"], raw["o2_b"])
@@ -202,7 +204,7 @@ def test_block_stagewise(pkg, dev, run):
     # FFN up + GELU + MX from the GPU's a3
     inter = snap["gemm_up"][0]
     up = oblock._deq(*_mx_np(a3)) @ oblock._deq(*wq["up"]).T + raw["up_b"].float()
-    _mx_close(inter, torch.nn.functional.gelu(up, approximate="tanh").to(torch.bfloat16), "FFN up + GELU (MX out)")
+    _mx_close(inter, torch.nn.functional.gelu(up, approximate="tanh").to(torch.bfloat16), "FFN up + GELU (MX out)", 0.995)
     # down projection + gated residual from the GPU's MX intermediate
     ffn = oblock._lin(*_mx_np(inter), wq["down"], raw["down_b"])
     ref_out = (h2.float().cpu() + ffn * c_gate).to(torch.bfloat16).float()

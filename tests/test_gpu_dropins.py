@@ -1,0 +1,207 @@
+"""The reference-form drop-ins, called as the reference's modules call them, against the oracle.
+
+- ``row_mx_qkv_proj`` as ``WanSelfAttentionFP8.forward`` calls it (row_mx_modules.py:340-404):
+  the ROW-packed activation of ``adaln_modulate(quant="row")``, the reference's packed
+  ``[H/4, I, 4]`` FP8 weight with Q/K channels de-interleaved per head, per-channel
+  ``weight_scales [1, I]`` (three checkpoint scalars expanded), a de-interleaved ``[1, I]`` bias and
+  ``[1, dim]`` gammas, rotate-half caches ``[B, S, 128]`` built from Wan's interleaved tables
+  (row_mx_modules.py:51-76), ``QKNormConfig(RMS_NORM_ACROSS_HEADS, RMS_NORM_ACROSS_HEADS)``, batch 2,
+  BSD and NBSd layouts; and as ``WanCrossAttentionFP8._project_query`` calls it (Q only, no RoPE,
+  NBSd). The oracle computes the ROW_MX projection (``psum * r_s * c_n + b``, qkv_cte.py:3996-4021)
+  in fp64 on the natural channel order, the across-heads RMSNorm and Wan's interleaved RoPE, and
+  the result is compared after de-interleaving its Q/K channels the same way.
+- ``row_mx_mlp`` with a ROW-packed input and per-channel ``*_w_scale`` against the oracle's
+  ROW_MX MLP (up -> GELU-tanh -> bf16 -> MX -> down, mlp_torch.py:471-597).
+- ``row_mx_o_proj`` on d-major ``[B, N, D, S]`` attention with the reference's partition-expanded
+  ``[128, H]`` weight scale against MX quantization of the token-major activation and the fp64
+  product.
+
+Bars: the GEMM bars of the projection tests (max |err| / max |ref| <= 2e-2, cosine >= 0.999) per
+output section; the NBSd result must be exactly the BSD result re-laid out.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as og
+from oracle import mx as omx
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+
+
+def _close(got, ref, what, bar=2e-2, cos_bar=0.999):
+    got, ref = got.double().flatten(), ref.double().flatten()
+    rel = float((got - ref).abs().max() / ref.abs().max())
+    cos = float(torch.nn.functional.cosine_similarity(got, ref, dim=0))
+    assert rel <= bar and cos >= cos_bar, (what, rel, cos)
+
+
+def _per_tensor_fp8(w: torch.Tensor):
+    """[K, N] fp32 -> (fp8 codes [K, N], scalar scale): absmax per-tensor quantization, as the
+    ComfyUI FP8-scaled checkpoint stores a linear."""
+    s = float(w.abs().max()) / 448.0
+    return (w / s).to(torch.float8_e4m3fn), s
+
+
+def _deinterleave_cols(n_heads: int) -> torch.Tensor:
+    perm = torch.cat([torch.arange(0, HD, 2), torch.arange(1, HD, 2)])
+    return (torch.arange(n_heads)[:, None] * HD + perm[None]).reshape(-1)
+
+
+def _pack(codes_kn: torch.Tensor) -> torch.Tensor:
+    """[K, N] fp8 -> the reference's [K/4, N, 4] (four consecutive contraction values innermost)."""
+    K, N = codes_kn.shape
+    return codes_kn.view(torch.uint8).reshape(K // 4, 4, N).permute(0, 2, 1).contiguous().view(torch.float8_e4m3fn)
+
+
+def _row_mx_oracle(packed: torch.Tensor, w_codes_kn: torch.Tensor, col_scale, bias) -> torch.Tensor:
+    """fp64 ROW_MX projection of a ROW-packed [T, K + 4] activation: (codes . dq_row) @ W * c + b."""
+    p = packed.reshape(-1, packed.shape[-1]).view(torch.uint8).cpu().numpy()
+    codes, dq = omx.row_unpack(p)
+    K = codes.shape[-1]
+    neutral_a = np.full((codes.shape[0], K // 32), 127, np.uint8)
+    wc = w_codes_kn.view(torch.uint8).t().contiguous().cpu().numpy()
+    neutral_w = np.full((wc.shape[0], K // 32), 127, np.uint8)
+    return og.mx_gemm(codes, neutral_a, wc, neutral_w, bias=bias, row_scale=dq.reshape(-1), col_scale=col_scale)
+
+
+@pytest.fixture(scope="module")
+def qkv_case(pkg, dev):
+    B, grid, nh = 2, (1, 15, 20), 8
+    S, dim = grid[0] * grid[1] * grid[2], nh * HD
+    g = torch.Generator().manual_seed(11)
+    h = torch.randn(B, S, dim, generator=g).to(torch.bfloat16)
+    mul, add = 1 + 0.5 * torch.randn(dim, generator=g), 0.5 * torch.randn(dim, generator=g)
+    wq, sq = _per_tensor_fp8(torch.randn(dim, dim, generator=g) * 0.02)
+    wk, sk = _per_tensor_fp8(torch.randn(dim, dim, generator=g) * 0.03)
+    wv, sv = _per_tensor_fp8(torch.randn(dim, dim, generator=g) * 0.01)
+    w_nat = torch.cat([wq, wk, wv], dim=1)  # [K, 3 dim], natural channel order
+    scales = torch.cat([torch.full((dim,), s) for s in (sq, sk, sv)])
+    bias = 0.1 * torch.randn(3 * dim, generator=g)
+    gq, gk = 1 + 0.1 * torch.randn(dim, generator=g), 1 + 0.1 * torch.randn(dim, generator=g)
+    # the reference loader's layout: Q/K columns de-interleaved per head, V untouched
+    qk_perm = _deinterleave_cols(nh)
+    order = torch.cat([qk_perm, dim + qk_perm, torch.arange(2 * dim, 3 * dim)])
+    w_ref = w_nat.view(torch.uint8)[:, order].contiguous().view(torch.float8_e4m3fn)
+    packed = pkg.adaln_modulate(h.to(dev), mul.to(dev), add.to(dev), eps=1e-6, quant="row")
+    cos, sin = orope.wan_rope(grid)
+    base_c, base_s = cos[:, 0::2], sin[:, 1::2]
+    cos_cache = torch.cat([base_c, base_c], -1)[None].expand(B, S, HD).contiguous()
+    sin_cache = torch.cat([base_s, base_s], -1)[None].expand(B, S, HD).contiguous()
+    # oracle, natural order: ROW_MX projection -> bf16 -> across-heads RMS -> interleaved RoPE
+    lin = _row_mx_oracle(packed, w_nat, scales.numpy(), bias.numpy()).float().to(torch.bfloat16).view(B, S, 3 * dim)
+    q = orope.rms_norm_across_heads(lin[..., :dim], gq).view(B, S, nh, HD)
+    k = orope.rms_norm_across_heads(lin[..., dim : 2 * dim], gk).view(B, S, nh, HD)
+    q = orope.apply_rotary_emb_wan(q, cos[None, :, None], sin[None, :, None]).view(B, S, dim)
+    k = orope.apply_rotary_emb_wan(k, cos[None, :, None], sin[None, :, None]).view(B, S, dim)
+    ref_nat = torch.cat([q, k, lin[..., 2 * dim :]], dim=-1)
+    return dict(B=B, S=S, nh=nh, dim=dim, packed=packed, w_ref=w_ref, w_nat=w_nat, order=order, scales=scales,
+                bias=bias, gq=gq, gk=gk, cos_cache=cos_cache, sin_cache=sin_cache, ref_nat=ref_nat, lin=lin)
+
+
+def _call_self(pkg, c, dev, weight, layout, scales, bias, gq, gk):
+    ct = pkg.common_types
+    return pkg.row_mx_qkv_proj(
+        c["packed"], weight, scales.to(dev)[None], bias.to(dev)[None], num_heads=c["nh"], head_dim=HD,
+        num_kv_heads=c["nh"], fused_rope=True, cos_cache=c["cos_cache"].to(dev), sin_cache=c["sin_cache"].to(dev),
+        qk_norm_pre_rope=ct.QKNormConfig(ct.NormType.RMS_NORM_ACROSS_HEADS, ct.NormType.RMS_NORM_ACROSS_HEADS, 1e-6),
+        qk_norm_pre_rope_q_gamma=gq.to(dev)[None], qk_norm_pre_rope_k_gamma=gk.to(dev)[None], norm_eps=1e-6,
+        output_layout=layout,
+    )
+
+
+def test_qkv_proj_reference_packed_weight(pkg, dev, qkv_case):
+    c = qkv_case
+    dim, order = c["dim"], c["order"]
+    ct = pkg.common_types
+    w = _pack(c["w_ref"]).to(dev)
+    out = _call_self(pkg, c, dev, w, None, c["scales"][order], c["bias"][order], c["gq"][order[:dim]],
+                     c["gk"][order[dim : 2 * dim] - dim])
+    assert out.shape == (c["B"], c["S"], 3 * dim) and out.dtype == torch.bfloat16
+    ref = c["ref_nat"][..., order]  # the reference's channel order
+    got = out.cpu()
+    for name, sl in (("Q", slice(0, dim)), ("K", slice(dim, 2 * dim)), ("V", slice(2 * dim, 3 * dim))):
+        for b in range(c["B"]):
+            _close(got[b, :, sl], ref[b, :, sl], f"{name} batch {b}")
+    # NBSd is the same result laid out [N, B, S, d]
+    nbsd = _call_self(pkg, c, dev, w, ct.QKVOutputLayout.NBSd, c["scales"][order], c["bias"][order],
+                      c["gq"][order[:dim]], c["gk"][order[dim : 2 * dim] - dim])
+    assert nbsd.shape == (3 * c["nh"], c["B"], c["S"], HD) and nbsd.is_contiguous()
+    assert torch.equal(nbsd.cpu(), got.view(c["B"], c["S"], 3 * c["nh"], HD).permute(2, 0, 1, 3))
+
+
+def test_qkv_proj_natural_order_mxweight(pkg, dev, qkv_case):
+    """The same projection from an MXWeight in Wan's natural order (interleaved RoPE pairs)."""
+    c = qkv_case
+    dim = c["dim"]
+    codes = c["w_nat"].view(torch.uint8).t().contiguous().view(torch.float8_e4m3fn).to(dev)
+    mw = pkg.MXWeight(codes, torch.full((3 * dim, dim // 32), 127, dtype=torch.uint8, device=dev))
+    out = _call_self(pkg, c, dev, mw, None, c["scales"], c["bias"], c["gq"], c["gk"]).cpu()
+    for name, sl in (("Q", slice(0, dim)), ("K", slice(dim, 2 * dim)), ("V", slice(2 * dim, 3 * dim))):
+        _close(out[:, :, sl], c["ref_nat"][:, :, sl], name)
+
+
+def test_cross_query_projection_nbsd(pkg, dev, qkv_case):
+    """``WanCrossAttentionFP8._project_query``: Q only (num_kv_heads 0), across-heads norm, no RoPE."""
+    c = qkv_case
+    dim, nh = c["dim"], c["nh"]
+    ct = pkg.common_types
+    wq = c["w_nat"][:, :dim]
+    out = pkg.row_mx_qkv_proj(
+        c["packed"], _pack(wq).to(dev), c["scales"][:dim].to(dev)[None], c["bias"][:dim].to(dev)[None], num_heads=nh,
+        head_dim=HD, qk_norm_pre_rope=ct.QKNormConfig(ct.NormType.RMS_NORM_ACROSS_HEADS, None, 1e-6),
+        qk_norm_pre_rope_q_gamma=c["gq"].to(dev)[None], norm_eps=1e-6, output_layout=ct.QKVOutputLayout.NBSd,
+    )
+    assert out.shape == (nh, c["B"], c["S"], HD)
+    ref = orope.rms_norm_across_heads(c["lin"][..., :dim], c["gq"]).view(c["B"], c["S"], nh, HD).permute(2, 0, 1, 3)
+    _close(out.cpu(), ref, "cross Q")
+
+
+def test_row_mx_mlp(pkg, dev):
+    B, S, dim, ffn = 2, 200, 1024, 2816
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(B, S, dim, generator=g).to(torch.bfloat16)
+    wu, su = _per_tensor_fp8(torch.randn(dim, ffn, generator=g) * 0.02)
+    wd, sd = _per_tensor_fp8(torch.randn(ffn, dim, generator=g) * 0.02)
+    bu, bd = 0.1 * torch.randn(ffn, generator=g), 0.1 * torch.randn(dim, generator=g)
+    packed = pkg.adaln_modulate(h.to(dev), eps=1e-6, quant="row")
+
+    def mxw(codes_kn):
+        n, k = codes_kn.shape[1], codes_kn.shape[0]
+        return pkg.MXWeight(codes_kn.view(torch.uint8).t().contiguous().view(torch.float8_e4m3fn).to(dev),
+                            torch.full((n, k // 32), 127, dtype=torch.uint8, device=dev))
+
+    up_scale = torch.full((1, ffn), su)
+    down_scale = torch.full((128, dim), sd)  # partition-expanded, as the reference loads it
+    out = pkg.row_mx_mlp(packed, mxw(wu), mxw(wd), up_scale.to(dev), down_scale.to(dev), bu.to(dev)[None],
+                         bd.to(dev)[None])
+    assert out.shape == (B, S, dim) and out.dtype == torch.bfloat16
+    up = _row_mx_oracle(packed, wu, np.full(ffn, su, np.float32), bu.numpy())
+    gel = og.gelu_tanh(up).float().to(torch.bfloat16).float().numpy()
+    ic, isc = omx.mx_quantize(gel)
+    wdc = wd.view(torch.uint8).t().contiguous().numpy()
+    ref = og.mx_gemm(ic, isc, wdc, np.full((dim, ffn // 32), 127, np.uint8), bias=bd.numpy(),
+                     col_scale=np.full(dim, sd, np.float32))
+    _close(out.cpu().view(B * S, dim), ref, "row_mx_mlp")
+
+
+def test_row_mx_o_proj(pkg, dev):
+    B, nh, S, dim = 2, 8, 300, 1024
+    g = torch.Generator().manual_seed(13)
+    att = torch.randn(B, nh, HD, S, generator=g).to(torch.bfloat16)  # d-major [B, N, D, S]
+    wo, so = _per_tensor_fp8(torch.randn(nh * HD, dim, generator=g) * 0.02)
+    bo = 0.1 * torch.randn(dim, generator=g)
+    codes = wo.view(torch.uint8).t().contiguous()
+    mw = pkg.MXWeight(codes.view(torch.float8_e4m3fn).to(dev),
+                      torch.full((dim, nh * HD // 32), 127, dtype=torch.uint8, device=dev))
+    out = pkg.row_mx_o_proj(att.to(dev), mw, torch.full((128, dim), so, device=dev), bo.to(dev)[None])
+    assert out.shape == (B, S, dim)
+    x = att.permute(0, 3, 1, 2).reshape(B * S, nh * HD).float().numpy()
+    xc, xs = omx.mx_quantize(x)
+    ref = og.mx_gemm(xc, xs, codes.numpy(), np.full((dim, nh * HD // 32), 127, np.uint8), bias=bo.numpy(),
+                     col_scale=np.full(dim, so, np.float32))
+    _close(out.cpu().view(B * S, dim), ref, "row_mx_o_proj")

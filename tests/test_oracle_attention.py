@@ -79,9 +79,45 @@ def test_rope_preserves_norm_and_matches_rotate_half():
     assert torch.allclose(y_rh.to(torch.float64), y[..., perm], atol=1e-6)
 
 
-def test_rms_norm_across_heads():
+def test_rms_norm_across_heads_unit_mean_square():
     g = torch.Generator().manual_seed(3)
     x = torch.randn(7, 512, generator=g).to(torch.bfloat16)
     w = torch.ones(512)
     y = orope.rms_norm_across_heads(x, w).float()
     assert torch.allclose(y.pow(2).mean(dim=-1), torch.ones(7), atol=2e-2)
+
+
+def test_rms_norm_is_across_heads_not_per_head():
+    """Heads at very different scales: one RMS over the whole row (DistributedRMSNorm at tp=1,
+    wan2_2_transformer.py:879-893) leaves their ratio intact; a per-head norm would make every
+    head unit-RMS. Closed form for a row whose head h holds the constant a_h over 128 channels:
+    y = a_h / sqrt(mean_h(a_h^2) + eps) * gamma."""
+    a = [8.0, 0.25, -2.0, 0.0]  # bf16-exact head values
+    x = torch.cat([torch.full((128,), v) for v in a])[None].to(torch.bfloat16)
+    gamma = torch.cat([torch.full((128,), gv) for gv in (1.0, 2.0, 0.5, 3.0)])
+    y = orope.rms_norm_across_heads(x, gamma).float()[0]
+    rms = math.sqrt(sum(v * v for v in a) / 4 + 1e-6)
+    for hd, (v, gv) in enumerate(zip(a, (1.0, 2.0, 0.5, 3.0))):
+        want = v / rms * gv
+        got = y[hd * 128 : (hd + 1) * 128]
+        assert bool((got == got[0]).all())
+        assert abs(float(got[0]) - want) <= 2.0**-8 * abs(want) + 1e-30, (hd, float(got[0]), want)
+    # a per-head norm would give head 1 the value 2.0 (unit RMS times gamma 2); across heads it is
+    # 0.25 / 4.14 * 2 = 0.12
+    assert float(y[128]) < 0.2
+
+
+def test_rms_norm_eps_inside_the_root():
+    """A constant row c with c^2 comparable to eps: y = c / sqrt(c^2 + eps) * gamma. Dropping eps
+    gives 1.0 and adding it outside the root (c / (|c| + eps)) gives 0.999; the closed form is
+    1 / sqrt(2) = 0.7071 here."""
+    c = 2.0**-10  # c^2 = 2^-20 ~ 9.5e-7 ~ eps
+    eps = 2.0**-20
+    x = torch.full((1, 256), c).to(torch.bfloat16)
+    y = orope.rms_norm_across_heads(x, torch.ones(256), eps).float()
+    assert abs(float(y[0, 0]) - 2.0**-0.5) <= 2.0**-8, float(y[0, 0])
+    # eps as given (1e-6 in the Wan config) on a row of 1e-3: 1e-3 / sqrt(1e-6 + 1e-6)
+    x = torch.full((1, 256), 1e-3).to(torch.bfloat16)
+    y = orope.rms_norm_across_heads(x, torch.ones(256), 1e-6).float()
+    xv = float(x[0, 0].float())
+    assert abs(float(y[0, 0]) - xv / math.sqrt(xv * xv + 1e-6)) <= 2.0**-8

@@ -33,7 +33,8 @@ _SIGNATURES = {
     "wanmi_adaln_quant": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp, _vp, _vp, _vp],
     "wanmi_e4m3_encode": [_vp, _vp, _i64, _vp],
     "wanmi_mxfp8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp],
-    "wanmi_qk_rmsnorm_rope": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _f32, _vp, _vp],
+    "wanmi_qk_rmsnorm_rope": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp],
+    "wanmi_rope_tables": [_i64, _i64, _i64, _i32, _i64, ctypes.c_double, _i32, _vp, _vp, _vp],
     "wanmi_transpose_heads": [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "wanmi_head_max_norm": [_vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "wanmi_mxfp8_gemm_rowsumsq": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
@@ -97,6 +98,28 @@ def ptr(t: torch.Tensor | None):
 def stream_of(t: torch.Tensor):
     """The current HIP stream of ``t``'s device, as the void* the C ABI takes."""
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def expect(t: torch.Tensor | None, what: str, *, dtype: torch.dtype, shape: tuple | None = None,
+           contiguous: bool = True, optional: bool = False, row_contiguous: bool = False) -> None:
+    """Host-side check of one tensor whose pointer goes to the C ABI: dtype, exact shape (None
+    entries match any size) and memory layout. Raises ValueError before anything is launched."""
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"{what} is required")
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{what} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise ValueError(f"{what} must be {dtype}, got {t.dtype}")
+    if shape is not None:
+        if t.dim() != len(shape) or any(want is not None and have != want for have, want in zip(t.shape, shape)):
+            want = "[" + ", ".join("*" if w is None else str(w) for w in shape) + "]"
+            raise ValueError(f"{what} must have shape {want}, got {list(t.shape)}")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if row_contiguous and t.dim() >= 1 and t.shape[-1] > 1 and t.stride(-1) != 1:
+        raise ValueError(f"{what} must have unit stride along its last dimension")
 
 
 def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:

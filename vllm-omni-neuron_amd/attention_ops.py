@@ -28,7 +28,7 @@ import torch
 from . import _lib
 from .adaln_kernels import adaln_quant_2d
 from .common_types import MXTensor, NormType, QKVOutputLayout
-from .row_mx_kernels import MXWeight, _with, mxfp8_linear
+from .row_mx_kernels import MXWeight, _with, mxfp8_linear  # noqa: F401
 
 HEAD_DIM = 128
 OUT_TOKEN, OUT_DMAJOR, OUT_MX = 0, 1, 2
@@ -46,22 +46,45 @@ def rope_pair_tables(cos: torch.Tensor, sin: torch.Tensor):
     return c.to(torch.float32).contiguous(), s.to(torch.float32).contiguous()
 
 
+_ROTATE = {"interleaved": 0, "halves": 1}
+
+
+def _check_rope_tables(cos, sin, S: int, what: str) -> None:
+    """cos / sin: both None, or fp32 contiguous ``[S, 64]`` pair tables for the S rows."""
+    if (cos is None) != (sin is None):
+        raise ValueError(f"{what}: cos and sin must both be given or both be None")
+    if cos is not None:
+        _lib.expect(cos, f"{what}: cos", dtype=torch.float32, shape=(S, HEAD_DIM // 2))
+        _lib.expect(sin, f"{what}: sin", dtype=torch.float32, shape=(S, HEAD_DIM // 2))
+
+
 def qk_rmsnorm_rope_(x: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None, eps: float = 1e-6,
-                     want_max: bool = False):
+                     want_max: bool = False, rope_pairs: str = "interleaved"):
     """In place on a bf16 ``[S, heads*128]`` view (unit column stride): across-heads RMSNorm * gamma,
-    then interleaved RoPE with pair tables ``cos``/``sin`` ``[S, 64]`` when given. Returns the
-    per-head max key norm ``[heads]`` (fp32) when ``want_max``."""
+    then RoPE with pair tables ``cos``/``sin`` fp32 ``[S, 64]`` when given, on the channel pairs
+    ``rope_pairs`` names (``"interleaved"``: (2i, 2i+1); ``"halves"``: (i, i+64), the rotate-half
+    order of de-interleaved channels). Returns the per-head max norm ``[heads]`` (fp32) when
+    ``want_max``."""
     lib = _lib.load()
-    _lib.require_gpu(x, gamma, cos, sin, what="qk_rmsnorm_rope")
-    if x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.bfloat16:
+    if rope_pairs not in _ROTATE:
+        raise ValueError(f"unknown rope_pairs {rope_pairs!r}")
+    if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.bfloat16:
         raise ValueError("x must be a bf16 [S, heads*128] view with unit column stride")
     S, W = x.shape
+    if W % (4 * HEAD_DIM):
+        raise ValueError(f"x width {W} must be a multiple of {4 * HEAD_DIM} (heads a multiple of 4)")
+    if x.stride(0) % 8 or x.data_ptr() % 16:
+        raise ValueError("x rows must be 16-byte aligned")
     heads = W // HEAD_DIM
+    if not isinstance(gamma, torch.Tensor) or gamma.numel() != W or not gamma.is_floating_point():
+        raise ValueError(f"gamma must be a floating-point tensor of {W} elements")
+    _check_rope_tables(cos, sin, S, "qk_rmsnorm_rope")
+    _lib.require_gpu(x, gamma, cos, sin, what="qk_rmsnorm_rope")
     gamma = gamma.reshape(W).to(torch.float32).contiguous()
     kmax = torch.empty(heads, dtype=torch.float32, device=x.device) if want_max else None
     st = lib.wanmi_qk_rmsnorm_rope(
-        _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), float(eps),
-        _lib.ptr(kmax), _lib.stream_of(x),
+        _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), _ROTATE[rope_pairs],
+        float(eps), _lib.ptr(kmax), _lib.stream_of(x),
     )
     _lib.check(st, "wanmi_qk_rmsnorm_rope")
     return kmax
@@ -114,11 +137,35 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
     projection and the kernel applies the across-heads RMSNorm (and RoPE) to it on load, exactly as
     :func:`qk_rmsnorm_rope_` would in a separate pass."""
     lib = _lib.load()
-    _lib.require_gpu(q, k, vt, kmax, what="attention")
+    if q.dim() != 3 or k.dim() != 3 or q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise ValueError("q, k must be bf16 [S, N, 128] views")
     Sq, N, D = q.shape
     Sk = k.shape[0]
     if D != HEAD_DIM or k.shape[1:] != (N, D) or q.stride(2) != 1 or k.stride(2) != 1:
         raise ValueError("q, k must be [S, N, 128] with unit d stride and matching heads")
+    _lib.expect(vt, "vt", dtype=torch.bfloat16, shape=(N, D, None))
+    if vt.shape[-1] < Sk or vt.shape[-1] % 64:
+        raise ValueError(f"vt must be [N, 128, S_pad] with S_pad >= {Sk} a multiple of 64 (transpose_heads)")
+    _lib.expect(kmax, "kmax", dtype=torch.float32, shape=(N,))
+    if out is not None:
+        if out_mode == OUT_TOKEN:
+            _lib.expect(out, "out", dtype=torch.bfloat16, shape=(Sq, N * D), contiguous=False, row_contiguous=True)
+        elif out_mode == OUT_DMAJOR:
+            _lib.expect(out, "out", dtype=torch.bfloat16, shape=(N, D, Sq), contiguous=False, row_contiguous=True)
+        else:
+            _lib.expect(out, "out", dtype=torch.uint8, shape=(Sq, N * D), contiguous=False, row_contiguous=True)
+    if out_mode not in (OUT_TOKEN, OUT_DMAJOR, OUT_MX):
+        raise ValueError(f"unknown out_mode {out_mode}")
+    if q_prep is not None:
+        _lib.expect(q_prep.sumsq, "q_prep.sumsq", dtype=torch.float32, shape=(Sq, None), contiguous=False,
+                    row_contiguous=True)
+        if q_prep.sumsq.shape[1] < N:
+            raise ValueError(f"q_prep.sumsq needs at least {N} partial sums per row")
+        if not isinstance(q_prep.gamma, torch.Tensor) or q_prep.gamma.numel() != N * D:
+            raise ValueError(f"q_prep.gamma must hold {N * D} elements")
+        _check_rope_tables(q_prep.cos, q_prep.sin, Sq, "attention q_prep")
+        _lib.require_gpu(q_prep.sumsq, q_prep.gamma, q_prep.cos, q_prep.sin, what="attention")
+    _lib.require_gpu(q, k, vt, kmax, out, what="attention")
     dev = q.device
     scales = None
     if out_mode == OUT_TOKEN:
@@ -141,9 +188,6 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
         _lib.check(st, "wanmi_attention_const_max")
     else:
         ss = q_prep.sumsq
-        _lib.require_gpu(ss, q_prep.gamma, q_prep.cos, q_prep.sin, what="attention")
-        if ss.dim() != 2 or ss.shape[0] != Sq or ss.stride(1) != 1 or ss.dtype != torch.float32:
-            raise ValueError("q_prep.sumsq must be fp32 [Sq, blocks] with unit column stride")
         gamma = q_prep.gamma.reshape(-1).to(torch.float32).contiguous()
         st = lib.wanmi_attention_const_max_qprep(
             *common, _lib.ptr(ss), ss.stride(0), _lib.ptr(gamma), _lib.ptr(q_prep.cos), _lib.ptr(q_prep.sin),
@@ -201,15 +245,35 @@ def ring_attention_const_max_fwd(q, k, v, replica_groups=None, num_workers=1, so
     return torch.stack(outs, dim=0)
 
 
+def _base_angles(cache: torch.Tensor, B: int, S: int, what: str) -> list[torch.Tensor]:
+    """Rotate-half cache ``[B, S, 128]`` (or ``[S, 128]``, ``[1, S, 128]``) = ``cat([base, base])``
+    (row_mx_modules.py:51-76) -> per batch element the fp32 ``[S, 64]`` base angles."""
+    if not isinstance(cache, torch.Tensor) or cache.shape[-1] != HEAD_DIM or cache.dim() not in (2, 3):
+        raise ValueError(f"{what} must be [B, S, {HEAD_DIM}] (rotate-half cache)")
+    c = cache if cache.dim() == 3 else cache.unsqueeze(0)
+    if c.shape[1] != S or c.shape[0] not in (1, B):
+        raise ValueError(f"{what} must be [{B}, {S}, {HEAD_DIM}], got {list(cache.shape)}")
+    return [c[min(b, c.shape[0] - 1), :, : HEAD_DIM // 2].to(torch.float32).contiguous() for b in range(B)]
+
+
+def _norm_kind(kind, what: str) -> bool:
+    """True for the across-heads RMSNorm, False for none; anything else is not on the Wan path."""
+    if kind is None or kind == NormType.NO_NORM:
+        return False
+    if kind == NormType.RMS_NORM_ACROSS_HEADS:
+        return True
+    raise NotImplementedError(f"{what}={kind} is not supported (the Wan path uses RMS_NORM_ACROSS_HEADS)")
+
+
 def row_mx_qkv_proj(
     packed_hidden,
-    weight: MXWeight,
+    weight,
     weight_scales: torch.Tensor | None = None,
     bias: torch.Tensor | None = None,
     *,
     num_heads: int,
     head_dim: int,
-    num_kv_heads: int,
+    num_kv_heads: int = 0,
     fused_rope: bool = False,
     cos_cache: torch.Tensor | None = None,
     sin_cache: torch.Tensor | None = None,
@@ -222,47 +286,80 @@ def row_mx_qkv_proj(
 ):
     """Fused ``[Q | K | V]`` projection with the across-heads QK RMSNorm and RoPE applied to Q/K.
 
-    ``cos_cache``/``sin_cache`` are the reference's rotate-half caches ``[B, S, head_dim]``
-    (``cat([base, base])``, row_mx_modules.py:51-76); the rotation is applied to Wan's interleaved
-    channel pairs directly, so weights and gammas stay in their natural channel order (the reference
-    de-interleaves them offline instead, row_mx_loaders.py:26-99). Q.K is identical either way.
-    Returns bf16 ``[B, S, (nq + 2 nkv) * d]`` (BSD) or ``[N, B, S, d]`` (NBSd).
+    ``packed_hidden``: the ROW-packed ``[B, S, H + 4]`` activation (``adaln_modulate(quant="row")``)
+    or an :class:`MXTensor`. ``weight``: the reference's packed ``[H/4, I, 4]`` float8_e4m3fn weight
+    (Q/K channels de-interleaved per head, as its loader stores them) or an :class:`MXWeight`;
+    ``weight_scales`` ``[1, I]`` and ``bias`` ``[1, I]`` as the reference passes them.
+    ``cos_cache``/``sin_cache`` are the rotate-half caches ``[B, S, head_dim]`` (``cat([base,
+    base])``, row_mx_modules.py:51-76). RoPE rotates the channel pairs of the weight's order: the
+    halves (i, i+64) for the reference's de-interleaved weight (rotate-half, as its kernel does),
+    Wan's interleaved pairs for an :class:`MXWeight` in natural order (``rope_pairs``). Either way
+    Q.K equals Wan's interleaved RoPE. Returns bf16 ``[B, S, (nq + 2 nkv) * d]`` (BSD) or
+    ``[nq + 2 nkv, B, S, d]`` (NBSd), in the weight's channel order.
     """
+    from .row_mx_kernels import packed_weight_to_mx
+
     if head_dim != HEAD_DIM:
-        raise NotImplementedError(f"head_dim must be 128, got {head_dim}")
+        raise NotImplementedError(f"head_dim must be {HEAD_DIM}, got {head_dim}")
     if replica_groups:
         raise NotImplementedError("tensor-parallel replica groups span several GPUs")
-    y = mxfp8_linear(packed_hidden, _with(weight, weight_scales, bias))
-    lead = y.shape[:-1]
-    y2 = y.reshape(-1, y.shape[-1])
+    if output_layout not in (None, QKVOutputLayout.BSD, QKVOutputLayout.NBSd):
+        raise ValueError(f"unknown output_layout {output_layout}")
+    w = packed_weight_to_mx(weight, weight_scales, bias) if isinstance(weight, torch.Tensor) else _with(
+        weight, weight_scales, bias)
     nq, nkv = num_heads, num_kv_heads
-    cos = sin = None
-    if fused_rope:
-        half = head_dim // 2
-        cos = cos_cache.reshape(-1, cos_cache.shape[-2], head_dim)[0, :, :half].to(torch.float32).contiguous()
-        sin = sin_cache.reshape(-1, sin_cache.shape[-2], head_dim)[0, :, :half].to(torch.float32).contiguous()
-        if lead.numel() // max(lead[-1], 1) != 1:
-            raise NotImplementedError("fused RoPE with batch > 1")
+    width = (nq + 2 * nkv) * head_dim
+    if w.out_features != width:
+        raise ValueError(f"weight has {w.out_features} output channels, expected (num_heads + 2 num_kv_heads) "
+                         f"* head_dim = {width}")
     norm = qk_norm_pre_rope
-    if norm is not None and norm.q_norm == NormType.RMS_NORM_ACROSS_HEADS:
-        qk_rmsnorm_rope_(y2[:, : nq * head_dim], qk_norm_pre_rope_q_gamma, cos=cos, sin=sin, eps=norm.eps)
-    elif fused_rope:
-        raise NotImplementedError("RoPE without the across-heads norm is not on the Wan path")
-    if nkv and norm is not None and norm.k_norm == NormType.RMS_NORM_ACROSS_HEADS:
-        k_view = y2[:, nq * head_dim : (nq + nkv) * head_dim]
-        qk_rmsnorm_rope_(k_view, qk_norm_pre_rope_k_gamma, cos=cos, sin=sin, eps=norm.eps)
+    eps = norm.eps if norm is not None else norm_eps
+    norm_q = _norm_kind(norm.q_norm if norm is not None else None, "q_norm")
+    norm_k = nkv > 0 and _norm_kind(norm.k_norm if norm is not None else None, "k_norm")
+    if norm_q and qk_norm_pre_rope_q_gamma is None:
+        raise ValueError("the Q norm needs qk_norm_pre_rope_q_gamma")
+    if norm_k and qk_norm_pre_rope_k_gamma is None:
+        raise ValueError("the K norm needs qk_norm_pre_rope_k_gamma")
+    if fused_rope and not (norm_q and (nkv == 0 or norm_k)):
+        # the rotation rides on the norm pass; the Wan self-attention always normalizes both
+        raise NotImplementedError("fused RoPE is applied together with the across-heads Q and K norms")
+
+    y = mxfp8_linear(packed_hidden, w)
+    lead = y.shape[:-1]
+    B, S = (1, lead[0]) if len(lead) == 1 else (math.prod(lead[:-1]), lead[-1])
+    y2 = y.reshape(B * S, width)
+    cos = sin = [None] * B
+    if fused_rope:
+        if cos_cache is None or sin_cache is None:
+            raise ValueError("fused_rope needs cos_cache and sin_cache")
+        cos = _base_angles(cos_cache, B, S, "cos_cache")
+        sin = _base_angles(sin_cache, B, S, "sin_cache")
+    for b in range(B):  # the caches may differ per batch element; the norm is per row
+        rows = y2[b * S : (b + 1) * S]
+        if norm_q:
+            qk_rmsnorm_rope_(rows[:, : nq * head_dim], qk_norm_pre_rope_q_gamma, cos=cos[b], sin=sin[b], eps=eps,
+                             rope_pairs=w.rope_pairs)
+        if norm_k:
+            qk_rmsnorm_rope_(rows[:, nq * head_dim : (nq + nkv) * head_dim], qk_norm_pre_rope_k_gamma, cos=cos[b],
+                             sin=sin[b], eps=eps, rope_pairs=w.rope_pairs)
     if output_layout == QKVOutputLayout.NBSd:
-        n_total = y.shape[-1] // head_dim
-        return y.reshape(*lead, n_total, head_dim).movedim(-2, 0)
+        return y.reshape(*lead, width // head_dim, head_dim).movedim(-2, 0).contiguous()
     return y
 
 
 def row_mx_o_proj(attention: torch.Tensor, weight: MXWeight, weight_scales: torch.Tensor | None = None,
                   bias: torch.Tensor | None = None) -> torch.Tensor:
     """d-major bf16 attention ``[B, N, D, S]`` -> ``[B, S, H]``: the activation is MX-quantized along
-    N*D (the reference's kernel quantizes it internally) and projected with the MXFP8 GEMM."""
+    N*D (the reference's kernel quantizes it internally) and projected with the MXFP8 GEMM.
+    ``weight_scales`` ``[P, H]`` / ``[1, H]`` / ``[H]`` (the reference expands its scalar scale over
+    partitions, row_mx_modules.py:243-250) and ``bias`` ``[1, H]`` override the weight's own."""
+    if not isinstance(attention, torch.Tensor) or attention.dim() != 4 or attention.dtype != torch.bfloat16:
+        raise ValueError("attention must be bf16 [B, N, D, S]")
+    w = _with(weight, weight_scales, bias)
     B, N, D, S = attention.shape
+    if N * D != w.in_features:
+        raise ValueError(f"attention has N*D = {N * D} channels, the weight contracts {w.in_features}")
     x = attention.permute(0, 3, 1, 2).reshape(B * S, N * D).contiguous()
     xq = adaln_quant_2d(x, None, None, eps=0.0, norm_type="none", quant="mx")
-    y = mxfp8_linear(xq, _with(weight, weight_scales, bias))
+    y = mxfp8_linear(xq, w)
     return y.reshape(B, S, -1)

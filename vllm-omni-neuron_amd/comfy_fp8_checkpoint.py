@@ -89,18 +89,19 @@ FP8_TOP_LINEAR_MAP: dict[str, str] = {
     "head.head": "proj_out",
 }
 
-# Per-block quantized projections: (model module, model projection, checkpoint module prefix).
-# Self-attention Q/K/V fuse into one model parameter; the rest map one to one.
-_SELF_QKV = ("q", "k", "v")
-_BLOCK_LINEARS = (
-    ("attn1", "o", "self_attn.o"),
-    ("attn2", "q", "cross_attn.q"),
-    ("attn2", "k", "cross_attn.k"),
-    ("attn2", "v", "cross_attn.v"),
-    ("attn2", "o", "cross_attn.o"),
-    ("ffn", "up", "ffn.0"),
-    ("ffn", "down", "ffn.2"),
+# The quantized projections of one block: model module, model projection, and the checkpoint
+# linears whose output channels it concatenates (the fused self-attention QKV takes three).
+_PROJECTIONS: tuple[tuple[str, str, tuple[str, ...]], ...] = (
+    ("attn1", "qkv", ("self_attn.q", "self_attn.k", "self_attn.v")),
+    ("attn1", "o", ("self_attn.o",)),
+    ("attn2", "q", ("cross_attn.q",)),
+    ("attn2", "k", ("cross_attn.k",)),
+    ("attn2", "v", ("cross_attn.v",)),
+    ("attn2", "o", ("cross_attn.o",)),
+    ("ffn", "up", ("ffn.0",)),
+    ("ffn", "down", ("ffn.2",)),
 )
+_SELF_QKV = ("q", "k", "v")
 # Per-block plain tensors: model leaf -> checkpoint leaf (the three renames are the norm2/norm3 pair
 # and modulation -> scale_shift_table).
 _BLOCK_PLAIN = {
@@ -112,6 +113,11 @@ _BLOCK_PLAIN = {
     "norm2.bias": "norm3.bias",
     "scale_shift_table": "modulation",
 }
+# What every quantized linear must hold: leaf -> (safetensors dtype, accepted shapes or a rank).
+_QUANTIZED_LEAVES = {
+    "weight": (FP8_DTYPE_STR, 2),
+    "scale_weight": ("F32", ([], [1])),
+}
 
 
 def _check_native(native_fp8_modules: Collection[str]) -> frozenset:
@@ -122,24 +128,27 @@ def _check_native(native_fp8_modules: Collection[str]) -> frozenset:
     return native
 
 
+def _block_projections(num_layers: int):
+    """(model parameter prefix ``blocks.i.<module>.<proj>_proj``, module, checkpoint prefixes)."""
+    for i in range(num_layers):
+        for module, proj, sources in _PROJECTIONS:
+            yield f"blocks.{i}.{module}.{proj}_proj", module, tuple(f"blocks.{i}.{src}" for src in sources)
+
+
+def quantized_linear_prefixes(num_layers: int = NUM_BLOCKS) -> list[str]:
+    """Checkpoint prefixes of every FP8 linear the model consumes (per block, then the top level)."""
+    out = [src for _, _, sources in _block_projections(num_layers) for src in sources]
+    return out + list(FP8_TOP_LINEAR_MAP)
+
+
 def fp8_transformed_parameter_names(num_layers: int = NUM_BLOCKS,
                                     native_fp8_modules: Collection[str] = ()) -> list[str]:
-    """Model parameters produced from quantized checkpoint tensors: every projection weight, plus
-    the runtime per-channel scale parameters of the modules loaded natively (codes kept)."""
+    """Model parameters filled from quantized checkpoint tensors: the weight of every projection,
+    and for the modules loaded natively (codes kept) also their per-channel ``*_w_scale``."""
     native = _check_native(native_fp8_modules)
-    names: list[str] = []
-    for i in range(num_layers):
-        b = f"blocks.{i}"
-        names.append(f"{b}.attn1.qkv_proj_weight")
-        names += [f"{b}.{mod}.{proj}_proj_weight" for mod, proj, _ in _BLOCK_LINEARS]
-        if "attn1" in native:
-            names += [f"{b}.attn1.qkv_proj_w_scale", f"{b}.attn1.o_proj_w_scale"]
-        if "attn2" in native:
-            names += [f"{b}.attn2.{p}_proj_w_scale" for p in ("q", "k", "v", "o")]
-        if "ffn" in native:
-            names += [f"{b}.ffn.up_proj_w_scale", f"{b}.ffn.down_proj_w_scale"]
-    names += [f"{prefix}.weight" for prefix in FP8_TOP_LINEAR_MAP.values()]
-    return names
+    names = [f"{prefix}_weight" for prefix, _, _ in _block_projections(num_layers)]
+    names += [f"{prefix}_w_scale" for prefix, module, _ in _block_projections(num_layers) if module in native]
+    return names + [f"{model}.weight" for model in FP8_TOP_LINEAR_MAP.values()]
 
 
 def build_fp8_dequant_mappings(num_layers: int = NUM_BLOCKS) -> dict[str, str | list[str]]:
@@ -149,16 +158,13 @@ def build_fp8_dequant_mappings(num_layers: int = NUM_BLOCKS) -> dict[str, str | 
     keys ``[qW, qS, kW, kS, vW, vS]``); biases, norms and modulation map to one key each.
     """
     m: dict[str, str | list[str]] = {}
+    for prefix, _, sources in _block_projections(num_layers):
+        m[f"{prefix}_weight"] = [f"{src}.{leaf}" for src in sources for leaf in ("weight", "scale_weight")]
+        biases = [f"{src}.bias" for src in sources]
+        m[f"{prefix}_bias"] = biases if len(biases) > 1 else biases[0]
     for i in range(num_layers):
-        b = f"blocks.{i}"
-        m[f"{b}.attn1.qkv_proj_weight"] = [f"{b}.self_attn.{p}.{leaf}" for p in _SELF_QKV
-                                           for leaf in ("weight", "scale_weight")]
-        m[f"{b}.attn1.qkv_proj_bias"] = [f"{b}.self_attn.{p}.bias" for p in _SELF_QKV]
-        for mod, proj, src in _BLOCK_LINEARS:
-            m[f"{b}.{mod}.{proj}_proj_weight"] = [f"{b}.{src}.weight", f"{b}.{src}.scale_weight"]
-            m[f"{b}.{mod}.{proj}_proj_bias"] = f"{b}.{src}.bias"
         for model_leaf, ckpt_leaf in _BLOCK_PLAIN.items():
-            m[f"{b}.{model_leaf}"] = f"{b}.{ckpt_leaf}"
+            m[f"blocks.{i}.{model_leaf}"] = f"blocks.{i}.{ckpt_leaf}"
     m["patch_embedding.weight"] = "patch_embedding.weight"
     m["patch_embedding.bias"] = "patch_embedding.bias"
     m["scale_shift_table"] = "head.modulation"
@@ -174,51 +180,43 @@ def build_fp8_mappings(num_layers: int = NUM_BLOCKS,
     to its code tensor(s) only and a separate ``*_w_scale`` parameter to its scale key(s)."""
     native = _check_native(native_fp8_modules)
     m = build_fp8_dequant_mappings(num_layers)
-
-    def split(name: str) -> None:
-        src = m[name]
-        assert isinstance(src, list) and len(src) % 2 == 0
-        m[name] = src[0] if len(src) == 2 else src[0::2]
-        m[name.replace("_proj_weight", "_proj_w_scale")] = src[1] if len(src) == 2 else src[1::2]
-
-    for i in range(num_layers):
-        b = f"blocks.{i}"
-        if "attn1" in native:
-            split(f"{b}.attn1.qkv_proj_weight")
-            split(f"{b}.attn1.o_proj_weight")
-        if "attn2" in native:
-            for p in ("q", "k", "v", "o"):
-                split(f"{b}.attn2.{p}_proj_weight")
-        if "ffn" in native:
-            split(f"{b}.ffn.up_proj_weight")
-            split(f"{b}.ffn.down_proj_weight")
+    for prefix, module, sources in _block_projections(num_layers):
+        if module not in native:
+            continue
+        codes = [f"{src}.weight" for src in sources]
+        scales = [f"{src}.scale_weight" for src in sources]
+        m[f"{prefix}_weight"] = codes if len(codes) > 1 else codes[0]
+        m[f"{prefix}_w_scale"] = scales if len(scales) > 1 else scales[0]
     return m
 
 
+def _leaf_problems(header: Mapping[str, dict], key: str, dtype: str, shape_rule) -> list[str]:
+    entry = header.get(key)
+    if entry is None:
+        return [f"{key}: missing tensor"]
+    problems = []
+    if entry.get("dtype") != dtype:
+        problems.append(f"{key}: stored as {entry.get('dtype')}, the format requires {dtype}")
+    shape = entry.get("shape")
+    if isinstance(shape_rule, int):
+        if not isinstance(shape, list) or len(shape) != shape_rule:
+            problems.append(f"{key}: shape {shape} is not a 2-D [out, in] matrix")
+    elif shape not in shape_rule:
+        problems.append(f"{key}: shape {shape} is not a single scalar")
+    return problems
+
+
 def validate_fp8_checkpoint(header: Mapping[str, dict], num_layers: int = NUM_BLOCKS) -> None:
-    """Every quantized weight the mappings consume must be a 2-D ``F8_E4M3`` tensor with a scalar
-    ``F32`` ``scale_weight``; raises :class:`Fp8CheckpointError` naming the first offending key.
-    Checks the mapped contract, not the file's full tensor histogram, so reduced-layer files pass."""
-    m = build_fp8_dequant_mappings(num_layers)
-    for name in fp8_transformed_parameter_names(num_layers):
-        src = m[name]
-        if not isinstance(src, list) or len(src) % 2:
-            raise RuntimeError(f"invalid FP8 mapping for {name}: {src}")
-        for wkey, skey in zip(src[0::2], src[1::2]):
-            w = header.get(wkey)
-            if w is None:
-                raise Fp8CheckpointError(f"missing FP8 weight: {wkey}")
-            if w.get("dtype") != FP8_DTYPE_STR:
-                raise Fp8CheckpointError(f"{wkey} must be {FP8_DTYPE_STR}, got {w.get('dtype')}")
-            if len(w.get("shape", [])) != 2:
-                raise Fp8CheckpointError(f"{wkey} must be 2-D [out, in], got shape {w.get('shape')}")
-            s = header.get(skey)
-            if s is None:
-                raise Fp8CheckpointError(f"missing FP8 weight scale: {skey}")
-            if s.get("dtype") != "F32":
-                raise Fp8CheckpointError(f"{skey} must be F32, got {s.get('dtype')}")
-            if s.get("shape") not in ([], [1]):
-                raise Fp8CheckpointError(f"{skey} must be scalar, got shape {s.get('shape')}")
+    """Check the header against the format: every quantized linear the model consumes has a 2-D
+    ``F8_E4M3`` ``weight`` and a scalar ``F32`` ``scale_weight``. Raises :class:`Fp8CheckpointError`
+    listing every problem found (a reduced-layer file is checked against its own layer count)."""
+    problems = []
+    for prefix in quantized_linear_prefixes(num_layers):
+        for leaf, (dtype, shape_rule) in _QUANTIZED_LEAVES.items():
+            problems += _leaf_problems(header, f"{prefix}.{leaf}", dtype, shape_rule)
+    if problems:
+        shown = "; ".join(problems[:8]) + (f"; ... ({len(problems)} problems)" if len(problems) > 8 else "")
+        raise Fp8CheckpointError(f"not a Wan2.2 FP8-scaled checkpoint with {num_layers} blocks: {shown}")
 
 
 # ------------------------------------------------------------------------------------------------

@@ -2,8 +2,11 @@
 //
 // wanmi_qk_rmsnorm_rope: in place on a [S, heads*128] bf16 slab (row stride ld), per token:
 //   x_hat = bf16(x * rrms * gamma),  rrms = 1 / sqrt(sum(x^2) / (heads*128) + eps)     (across heads)
-//   then, if cos/sin are given, the interleaved RoPE of every (2i, 2i+1) pair in fp32:
+//   then, if cos/sin are given, RoPE in fp32 on the pairs (a, b) of each head -- interleaved
+//   channels (2i, 2i+1), Wan's own order, or the two halves (i, i+64), the rotate-half order of
+//   channels de-interleaved per head (row_mx_loaders.py:26-39, row_mx_modules.py:51-76):
 //   (a, b) -> bf16(a*cos - b*sin), bf16(a*sin + b*cos)
+//   The two give the same bits on correspondingly permuted channels.
 // and optionally the per-head maximum over tokens of ||x_out|| (the const-max bound's key norm).
 // Reference: DistributedRMSNorm.forward (vllm_omni_neuron/diffusion/models/wan2_2/
 // wan2_2_transformer.py:879-893) and apply_rotary_emb_wan (diffusion/layers/rope.py:8-34); the
@@ -47,7 +50,9 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // launch (8 tokens each) are then resident in one round over 256 CUs; at the 130 VGPRs the compiler
 // would otherwise take, only three waves per SIMD fit and the last quarter of the grid runs as a
 // second round (190 vs 159 us). Wider rows keep the registers they need.
-template <int NCH>
+// kHalves: rotate-half pairs (i, i+64) (the drop-in path for the reference's de-interleaved
+// weights; it keeps the register budget but may spill a little), else interleaved pairs.
+template <int NCH, bool kHalves>
 __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -88,18 +93,27 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
     ss = wave_sum_f32(ss);
     const float rs = (float)(1.0 / sqrt((double)(ss / (float)W) + (double)a.eps));
 
-    float cs[4], sn[4];
+    // interleaved: the lane's 4 pairs are the angles 4 (lane & 15) .. +3 of its head; halves: its 8
+    // channels 8 (lane & 15) .. +7 are first-half (lane & 8 == 0) or second-half channels whose angles
+    // are 8 (lane & 7) .. +7, paired with the same channels of lane ^ 8
+    constexpr int kAngles = kHalves ? 8 : 4;
+    float cs[kAngles], sn[kAngles];
     if (a.cos) {
       const __amdgpu_buffer_rsrc_t r_c = make_rsrc(a.cos + t * 64, 256);
       const __amdgpu_buffer_rsrc_t r_s = make_rsrc(a.sin + t * 64, 256);
-      const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(r_c, (lane & 15) * 16, 0, 0);
-      const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(r_s, (lane & 15) * 16, 0, 0);
+      const uint32_t off = kHalves ? (uint32_t)(lane & 7) * 32 : (uint32_t)(lane & 15) * 16;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        cs[j] = __uint_as_float(cv[j]);
-        sn[j] = __uint_as_float(sv[j]);
+      for (int u = 0; u < kAngles / 4; ++u) {
+        const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(r_c, off + 16 * u, 0, 0);
+        const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(r_s, off + 16 * u, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cs[4 * u + j] = __uint_as_float(cv[j]);
+          sn[4 * u + j] = __uint_as_float(sv[j]);
+        }
       }
     }
+    const bool second_half = (lane & 8) != 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (c < a.nch) {
@@ -110,21 +124,47 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
                              __uint_as_float(g1[2]), __uint_as_float(g1[3])};
         u32x4 ov;
         float n2 = 0.0f;
+        // normalized + gamma, rounded to bf16 (the reference rounds after the norm)
+        if constexpr (!kHalves) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // normalized + gamma, rounded to bf16 (the reference rounds after the norm)
-          float a0 = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
-          float b0 = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
-          if (a.cos) {
-            const float ac = a0 * cs[j], bs = b0 * sn[j], as = a0 * sn[j], bc = b0 * cs[j];
-            const float r0 = ac - bs, r1 = as + bc;
-            a0 = r0;
-            b0 = r1;
+          for (int j = 0; j < 4; ++j) {
+            float a0 = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
+            float b0 = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
+            if (a.cos) {
+              const float ac = a0 * cs[j], bs = b0 * sn[j], as = a0 * sn[j], bc = b0 * cs[j];
+              const float r0 = ac - bs, r1 = as + bc;
+              a0 = r0;
+              b0 = r1;
+            }
+            ov[j] = pack_bf16x2(a0, b0);
+            const float fa = bf16_lo(ov[j]), fb = bf16_hi(ov[j]);
+            n2 = n2 + fa * fa;
+            n2 = n2 + fb * fb;
           }
-          ov[j] = pack_bf16x2(a0, b0);
-          const float fa = bf16_lo(ov[j]), fb = bf16_hi(ov[j]);
-          n2 = n2 + fa * fa;
-          n2 = n2 + fb * fb;
+        } else {
+          float y[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            y[2 * j] = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
+            y[2 * j + 1] = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
+          }
+          if (a.cos) {
+            // pairs (i, i+64): first half x cos - x' sin, second half x cos + x' sin (x' = the
+            // partner channel, held by lane ^ 8)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float o = __shfl_xor(y[k], 8, 64);
+              const float xc = y[k] * cs[k], os = o * sn[k];
+              y[k] = second_half ? xc + os : xc - os;
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            ov[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
+            const float fa = bf16_lo(ov[j]), fb = bf16_hi(ov[j]);
+            n2 = n2 + fa * fa;
+            n2 = n2 + fb * fb;
+          }
         }
         __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
         if (a.maxnorm) {
@@ -215,7 +255,7 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(TransposeArgs a) {
 }  // namespace wanmi
 
 extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
-                                     const float* cos_tab, const float* sin_tab, float eps,
+                                     const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
                                      float* maxnorm, void* stream) {
   using namespace wanmi;
   clear_error();
@@ -226,6 +266,8 @@ extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, 
   WANMI_REQUIRE((cos_tab == nullptr) == (sin_tab == nullptr), WANMI_ERR_ARG,
                 "wanmi_qk_rmsnorm_rope: cos and sin must both be given or both be null");
   WANMI_REQUIRE(!(eps < 0.0f), WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope: eps must be >= 0");
+  WANMI_REQUIRE(rope_pairs == WANMI_ROTATE_INTERLEAVED || rope_pairs == WANMI_ROTATE_HALVES, WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope: unknown rope_pairs %d", rope_pairs);
   hipStream_t s = (hipStream_t)stream;
   if (maxnorm) {
     hipLaunchKernelGGL(zero_f32_kernel, dim3((heads + 255) / 256), dim3(256), 0, s, maxnorm, heads);
@@ -251,10 +293,17 @@ extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, 
   a.maxnorm = maxnorm;
   const int64_t waves = (S + a.tokens_per_wave - 1) / a.tokens_per_wave;
   const dim3 grid((unsigned)((waves + 3) / 4));
-  if (a.nch <= 4) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<4>, grid, dim3(256), 0, s, a);
-  else if (a.nch <= 10) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<10>, grid, dim3(256), 0, s, a);
-  else if (a.nch <= 16) hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<16>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<32>, grid, dim3(256), 0, s, a);
+  if (rope_pairs == WANMI_ROTATE_HALVES) {
+    if (a.nch <= 4) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<4, true>), grid, dim3(256), 0, s, a);
+    else if (a.nch <= 10) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<10, true>), grid, dim3(256), 0, s, a);
+    else if (a.nch <= 16) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<16, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<32, true>), grid, dim3(256), 0, s, a);
+  } else {
+    if (a.nch <= 4) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<4, false>), grid, dim3(256), 0, s, a);
+    else if (a.nch <= 10) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<10, false>), grid, dim3(256), 0, s, a);
+    else if (a.nch <= 16) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<16, false>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<32, false>), grid, dim3(256), 0, s, a);
+  }
   return check_launch("wanmi_qk_rmsnorm_rope");
 }
 

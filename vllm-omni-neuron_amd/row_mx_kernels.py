@@ -34,12 +34,17 @@ _NEUTRAL_SCALE = 127
 
 class MXWeight(NamedTuple):
     """A projection weight in GEMM layout: ``codes [N, K]`` e4m3fn, ``scales [N, K/32]`` e8m0,
-    an optional per-output-channel fp32 ``col_scale [N]`` (ROW_MX dequant) and fp32 ``bias [N]``."""
+    an optional per-output-channel fp32 ``col_scale [N]`` (ROW_MX dequant) and fp32 ``bias [N]``.
+
+    ``rope_pairs`` says how the Q/K output channels of a fused QKV weight pair up for RoPE:
+    ``"interleaved"`` (Wan's natural order, pairs (2i, 2i+1)) or ``"halves"`` (channels
+    de-interleaved per head as the reference's loader stores them, pairs (i, i+64))."""
 
     codes: torch.Tensor
     scales: torch.Tensor
     col_scale: torch.Tensor | None = None
     bias: torch.Tensor | None = None
+    rope_pairs: str = "interleaved"
 
     @property
     def out_features(self) -> int:
@@ -64,6 +69,33 @@ def quantize_weight_mx(weight_kn: torch.Tensor, bias: torch.Tensor | None = None
     return MXWeight(q.codes, q.scales, None, b)
 
 
+def packed_weight_to_mx(weight: torch.Tensor, weight_scales: torch.Tensor | None = None,
+                        bias: torch.Tensor | None = None, *, rope_pairs: str = "halves") -> MXWeight:
+    """The reference's packed ROW_MX projection weight ``[K/4, N, 4]`` float8_e4m3fn (four
+    consecutive contraction values innermost, row_mx_modules.py:299-301; ``[H, I]`` packed by
+    ``packed_fused_qkv_weight_loader``, row_mx_loaders.py:219-246) -> :class:`MXWeight`.
+
+    The codes are kept as they are (``[N, K]``, K-contiguous), the block scales are neutral (2^0)
+    and ``weight_scales`` (``[1, N]``, the checkpoint scalars expanded per channel) becomes the
+    per-channel ``col_scale`` of the epilogue -- the ROW_MX dequant ``psum * r_s * c_n``
+    (qkv_cte.py:3996-4021). The reference loader de-interleaves the Q/K channels of the fused
+    self-attention weight per head (row_mx_loaders.py:26-71), hence ``rope_pairs="halves"``."""
+    if weight.dim() != 3 or weight.shape[-1] != 4:
+        raise ValueError(f"packed weight must be [K/4, N, 4], got {list(weight.shape)}")
+    if weight.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError(f"packed weight must be float8_e4m3fn, got {weight.dtype}")
+    if rope_pairs not in ("interleaved", "halves"):
+        raise ValueError(f"unknown rope_pairs {rope_pairs!r}")
+    K4, N, _ = weight.shape
+    K = 4 * K4
+    if K % 32:
+        raise ValueError(f"contraction {K} must be a multiple of 32")
+    codes = weight.view(torch.uint8).permute(1, 0, 2).reshape(N, K).contiguous()
+    scales = torch.full((N, K // 32), _NEUTRAL_SCALE, dtype=torch.uint8, device=weight.device)
+    w = MXWeight(codes.view(torch.float8_e4m3fn), scales, None, None, rope_pairs)
+    return _with(w, weight_scales, bias)
+
+
 def _split_row_packed(packed: torch.Tensor):
     """Reference ROW-packed ``[T, K + 4]`` -> (codes [T, K], neutral scales, row scale [T])."""
     raw = packed.view(torch.uint8)
@@ -77,14 +109,39 @@ def _split_row_packed(packed: torch.Tensor):
 def _as_mx_2d(x):
     """MXTensor / ROW-packed tensor of any leading shape -> (codes2d, scales2d, row_scale, lead)."""
     if isinstance(x, MXTensor):
+        if x.codes.dtype not in (torch.float8_e4m3fn, torch.uint8):
+            raise ValueError(f"MX codes must be float8_e4m3fn, got {x.codes.dtype}")
         K = x.codes.shape[-1]
+        if K % 32:
+            raise ValueError(f"MX activation width {K} must be a multiple of 32")
         lead = x.codes.shape[:-1]
         codes = x.codes.reshape(-1, K).view(torch.uint8)
+        _lib.expect(x.scales, "activation scales", dtype=torch.uint8, shape=(*lead, K // 32), contiguous=False)
         scales = x.scales.reshape(-1, K // 32)
+        if codes.stride(1) != 1 or scales.stride(1) != 1:
+            raise ValueError("MX codes and scales must have unit stride along the last dimension")
         return codes, scales, None, lead
+    if not isinstance(x, torch.Tensor) or x.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError("the activation must be an MXTensor or a ROW-packed float8_e4m3fn tensor [..., K + 4]")
+    if x.shape[-1] < 36 or (x.shape[-1] - 4) % 32:
+        raise ValueError(f"ROW-packed width {x.shape[-1]} must be K + 4 with K a multiple of 32")
     lead = x.shape[:-1]
     codes, scales, row_scale = _split_row_packed(x.reshape(-1, x.shape[-1]))
     return codes, scales, row_scale, lead
+
+
+def _check_weight(weight: MXWeight, what: str = "weight") -> None:
+    if not isinstance(weight, MXWeight):
+        raise ValueError(f"{what} must be an MXWeight (see quantize_weight_mx / packed_weight_to_mx)")
+    N, K = weight.codes.shape if weight.codes.dim() == 2 else (None, None)
+    if N is None or weight.codes.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError(f"{what}.codes must be float8_e4m3fn [N, K], got {weight.codes.dtype} "
+                         f"{list(weight.codes.shape)}")
+    if not weight.codes.is_contiguous():
+        raise ValueError(f"{what}.codes must be contiguous")
+    _lib.expect(weight.scales, f"{what}.scales", dtype=torch.uint8, shape=(N, K // 32))
+    _lib.expect(weight.col_scale, f"{what}.col_scale", dtype=torch.float32, shape=(N,), optional=True)
+    _lib.expect(weight.bias, f"{what}.bias", dtype=torch.float32, shape=(N,), optional=True)
 
 
 def mxfp8_linear(
@@ -110,12 +167,37 @@ def mxfp8_linear(
     if epilogue not in EPILOGUES:
         raise ValueError(f"unknown epilogue {epilogue!r}")
     lib = _lib.load()
+    _check_weight(weight)
     codes, scales, row_scale, lead = _as_mx_2d(x)
     M, K = codes.shape
     N = weight.out_features
     if weight.in_features != K:
         raise ValueError(f"activation K={K} does not match weight K={weight.in_features}")
-    _lib.require_gpu(codes, weight.codes, residual, gate, what="mxfp8_linear")
+    res2 = None
+    if epilogue == "gated_residual":
+        if residual is None or gate is None:
+            raise ValueError("gated_residual needs residual and gate")
+        _lib.expect(residual, "residual", dtype=torch.bfloat16, contiguous=False)
+        if residual.numel() != M * N:
+            raise ValueError(f"residual must hold [{M}, {N}] elements, got {list(residual.shape)}")
+        res2 = residual.reshape(M, N).contiguous()
+        _lib.expect(gate, "gate", dtype=torch.float32, contiguous=False)
+        if gate.numel() != N:
+            raise ValueError(f"gate must hold {N} elements, got {gate.numel()}")
+        gate = gate.reshape(N).contiguous()
+    elif residual is not None or gate is not None:
+        raise ValueError("residual and gate belong to the gated_residual epilogue")
+    if out is not None:
+        want = torch.uint8 if epilogue == "gelu_mx" else torch.bfloat16
+        _lib.expect(out, "out", dtype=want, shape=(M, N), contiguous=False, row_contiguous=True)
+        if out.stride(0) % 16 or (epilogue == "gated_residual" and out.stride(0) != N):
+            raise ValueError("out must have a row stride that is a multiple of 16 (N for gated_residual)")
+    if row_sumsq is not None:
+        if epilogue != "bf16":
+            raise ValueError("row_sumsq needs the bf16 epilogue")
+        _lib.expect(row_sumsq, "row_sumsq", dtype=torch.float32, shape=(M, N // 128))
+    _lib.require_gpu(codes, scales, row_scale, weight.codes, weight.scales, weight.col_scale, weight.bias, res2,
+                     gate, out, row_sumsq, what="mxfp8_linear")
     dev = codes.device
     out_scales = None
     if epilogue == "gelu_mx":
@@ -123,18 +205,7 @@ def mxfp8_linear(
         out_scales = torch.empty((M, N // 32), dtype=torch.uint8, device=dev)
     else:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if out is None else out
-    res2 = None
-    if epilogue == "gated_residual":
-        if residual is None or gate is None:
-            raise ValueError("gated_residual needs residual and gate")
-        res2 = residual.reshape(M, N).contiguous()
-        gate = gate.reshape(N).to(torch.float32).contiguous()
     if row_sumsq is not None:
-        if epilogue != "bf16":
-            raise ValueError("row_sumsq needs the bf16 epilogue")
-        _lib.require_gpu(row_sumsq, what="mxfp8_linear")
-        if row_sumsq.shape != (M, N // 128) or row_sumsq.dtype != torch.float32 or not row_sumsq.is_contiguous():
-            raise ValueError(f"row_sumsq must be contiguous fp32 [{M}, {N // 128}]")
         status = lib.wanmi_mxfp8_gemm_rowsumsq(
             _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(weight.codes), _lib.ptr(weight.scales), _lib.ptr(row_scale),
             _lib.ptr(weight.col_scale), _lib.ptr(weight.bias), M, N, K, codes.stride(0), _lib.ptr(out), out.stride(0),
@@ -179,9 +250,11 @@ def row_mx_mlp(
 ):
     """Wan's gate-less GELU-tanh MLP: ``down(MX(GELU_tanh(up(x) + b_up))) + b_down``.
 
-    Same argument order as the reference (row_mx_kernels.py:141-149). ``*_w_scale`` are optional
-    per-output-channel fp32 dequant scales (the ROW_MX recipe); biases override the weights' own.
-    Returns bf16 ``[..., H]``.
+    Same argument order as the reference (row_mx_kernels.py:141-149). ``packed_hidden`` is the
+    ROW-packed ``[..., H + 4]`` activation of ``adaln_modulate(quant="row")`` or an :class:`MXTensor`.
+    ``*_w_scale`` are the per-output-channel fp32 dequant scales of the ROW_MX recipe (``[N]``,
+    ``[1, N]``, or the reference's partition-expanded ``[P, N]`` whose rows are equal; row 0 is used);
+    biases override the weights' own. Returns bf16 ``[..., H]``.
     """
     up = _with(up_weight, up_w_scale, up_bias)
     down = _with(down_weight, down_w_scale, down_bias)
@@ -189,7 +262,22 @@ def row_mx_mlp(
     return mxfp8_linear(inter, down, epilogue="bf16")
 
 
+def _channel_vector(t: torch.Tensor | None, n: int, what: str) -> torch.Tensor | None:
+    """A per-output-channel fp32 vector given as ``[n]``, ``[1, n]`` or ``[P, n]`` (rows equal; the
+    reference expands its scalar scales over partitions) -> contiguous fp32 ``[n]``."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor) or t.dim() == 0 or t.shape[-1] != n:
+        raise ValueError(f"{what} must be [{n}], [1, {n}] or [P, {n}], got "
+                         f"{list(t.shape) if isinstance(t, torch.Tensor) else type(t).__name__}")
+    if not t.is_floating_point():
+        raise ValueError(f"{what} must be floating point, got {t.dtype}")
+    return t.reshape(-1, n)[0].to(torch.float32).contiguous()
+
+
 def _with(w: MXWeight, col_scale, bias) -> MXWeight:
-    cs = w.col_scale if col_scale is None else col_scale.reshape(-1).to(torch.float32).contiguous()
-    b = w.bias if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
-    return MXWeight(w.codes, w.scales, cs, b)
+    _check_weight(w)
+    n = w.out_features
+    cs = w.col_scale if col_scale is None else _channel_vector(col_scale, n, "weight scale")
+    b = w.bias if bias is None else _channel_vector(bias, n, "bias")
+    return MXWeight(w.codes, w.scales, cs, b, w.rope_pairs)
