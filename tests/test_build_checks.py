@@ -1,9 +1,13 @@
-"""The build's check of the hot-loop direct-to-LDS loads (CPU).
+"""The build's checks of the generated code (CPU): hot-loop direct-to-LDS loads and wide stores.
 
 A vector instruction that writes an SGPR (a spill reload by v_readlane, v_readfirstlane) needs five
 wait states before a vector memory instruction reads that SGPR; the compiler does not check inline
 asm. The hot loads carry one wait state (M0's), so the build scans the generated code and falls back
 to five everywhere if a load could read a freshly written resource or offset.
+
+A store wider than 64 bits reads its data registers after it issues; a VALU write to one of them
+right after the store (seen in the compiler's output for the adaLN bf16 store, where some lanes then
+stored the new value) fails the build.
 """
 
 import importlib.util
@@ -54,3 +58,21 @@ def test_block_boundary_inside_the_window_is_a_hazard():
 def test_ordinary_loads_are_not_checked():
     asm = _asm("v_readfirstlane_b32 s45, v3", "buffer_load_dwordx4 v[0:3], v1, s[44:47], 0 offen")
     assert build.dma_sgpr_hazards(asm) == []
+
+
+def test_store_data_overwritten_right_after_a_wide_store():
+    asm = _asm("buffer_store_dwordx4 v[46:49], v61, s[36:39], s12 offen", "v_mov_b32_e32 v47, v1")
+    assert len(build.store_data_hazards(asm)) == 1
+    asm = _asm("global_store_dwordx4 v[2:3], v[8:11], off", "s_nop 0", "v_add_f32_e32 v11, v1, v2")
+    assert len(build.store_data_hazards(asm)) == 1
+
+
+def test_store_data_hazard_cleared_by_wait_states_or_other_registers():
+    asm = _asm("buffer_store_dwordx4 v[46:49], v61, s[36:39], s12 offen", "s_nop 1", "v_mov_b32_e32 v47, v1")
+    assert build.store_data_hazards(asm) == []
+    asm = _asm("buffer_store_dwordx4 v[46:49], v61, s[36:39], 0 offen", "v_mov_b32_e32 v50, v1",
+               "v_mov_b32_e32 v51, v1", "v_mov_b32_e32 v46, v1")
+    assert build.store_data_hazards(asm) == []
+    # 64-bit stores are not affected
+    asm = _asm("buffer_store_dwordx2 v[48:49], v63, s[36:39], 0 offen", "v_mov_b32_e32 v48, 0")
+    assert build.store_data_hazards(asm) == []

@@ -51,7 +51,9 @@ def _perm_cols(Nh, dev):
 
 def test_rotate_half_pairs_equal_interleaved_on_permuted_channels(pkg, dev):
     """Bit for bit on inputs whose sums of squares are exact in fp32 (multiples of 2^-3 up to 1,
-    so the row sums do not depend on the order in which the permuted lanes add them)."""
+    so the row sums do not depend on the order in which the permuted lanes add them). The per-head
+    key-norm maxima sum squares of the rotated outputs, whose order the permutation changes, so
+    they agree to fp32 rounding."""
     ops = pkg.attention_ops
     S, Nh = 1560, 40
     g = torch.Generator(device=dev).manual_seed(5)
@@ -64,7 +66,7 @@ def test_rotate_half_pairs_equal_interleaved_on_permuted_channels(pkg, dev):
     b = x[:, cols].contiguous()
     kb = ops.qk_rmsnorm_rope_(b, gamma[cols], cos=c, sin=s, want_max=True, rope_pairs="halves")
     assert torch.equal(b, a[:, cols])
-    assert torch.equal(ka, kb)
+    assert bool(((ka - kb).abs() <= 1e-6 * ka).all())
 
 
 def test_rotate_half_pairs_against_the_oracle(pkg, dev):

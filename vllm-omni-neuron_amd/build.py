@@ -88,6 +88,52 @@ def dma_sgpr_hazards(asm: str, window: int = 5) -> list[str]:
     return found
 
 
+_VREG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
+
+
+def _vgprs(text: str) -> set[int]:
+    out: set[int] = set()
+    for m in _VREG.finditer(text):
+        if m.group(1):
+            out |= set(range(int(m.group(1)), int(m.group(2)) + 1))
+        else:
+            out.add(int(m.group(3)))
+    return out
+
+
+def store_data_hazards(asm: str, window: int = 2) -> list[str]:
+    """Vector stores wider than 64 bits in `asm` (gfx950 device assembly) whose data VGPRs a VALU
+    instruction overwrites fewer than `window` wait states later. The store reads its data after it
+    issues; overwritten too soon, some lanes store the new value. The compiler's own hazard check has
+    missed this (an adaLN store followed directly by a move into one of its data registers), so
+    every kernel's generated code is checked."""
+    lines = [ln.split(";")[0].strip() for ln in asm.splitlines()]
+    found = []
+    for i, ln in enumerate(lines):
+        op = ln.split()[0] if ln else ""
+        if not op.startswith(("buffer_store", "global_store", "flat_store", "scratch_store")):
+            continue
+        if not any(w in op for w in ("dwordx3", "dwordx4", "b96", "b128")):
+            continue
+        operands = [o.strip() for o in ln[len(op):].split(",")]
+        data = _vgprs(operands[0] if op.startswith("buffer") else operands[1])
+        states, j = 0, i + 1
+        while states < window and j < len(lines):
+            nxt = lines[j]
+            j += 1
+            if not nxt or nxt.startswith((".", "#")) or nxt.endswith(":"):
+                continue
+            nop = nxt.split()[0]
+            if nop == "s_nop":
+                states += int(nxt.split()[1], 0) + 1
+                continue
+            if nop.startswith("v_") and _vgprs(nxt[len(nop):].split(",")[0]) & data:
+                found.append(f"{ln}  (then {nxt}, {states} wait states)")
+                break
+            states += 1
+    return found
+
+
 def _compile_once(src: pathlib.Path, obj: pathlib.Path, extra: list[str]) -> None:
     cmd = [_hipcc(), *HIP_FLAGS, *extra, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -105,18 +151,23 @@ def _device_asm(src: pathlib.Path, extra: list[str]) -> str:
 
 
 def _compile(src: pathlib.Path) -> pathlib.Path:
-    """Compiles one source. A source with hot-loop direct-to-LDS loads (one wait state) is checked
-    in its generated code; if any load may read an SGPR a vector instruction just wrote, the source
-    is rebuilt with WANMI_DMA_ALL_WAITS (five wait states everywhere) and checked again."""
+    """Compiles one source and checks its generated code. A source with hot-loop direct-to-LDS loads
+    (one wait state) is rebuilt with WANMI_DMA_ALL_WAITS (five wait states everywhere) if any load may
+    read an SGPR a vector instruction just wrote. A wide store whose data registers are overwritten
+    too soon fails the build."""
     obj = BUILD_DIR / (src.stem + ".o")
     _compile_once(src, obj, [])
-    if "lds_dma_b128_hot" in src.read_text():
-        if dma_sgpr_hazards(_device_asm(src, [])):
-            safe = ["-DWANMI_DMA_ALL_WAITS"]
-            _compile_once(src, obj, safe)
-            left = dma_sgpr_hazards(_device_asm(src, safe))
-            if left:
-                raise RuntimeError(f"{src.name}: direct-to-LDS loads read freshly written SGPRs:\n" + "\n".join(left[:5]))
+    asm = _device_asm(src, [])
+    if "lds_dma_b128_hot" in src.read_text() and dma_sgpr_hazards(asm):
+        safe = ["-DWANMI_DMA_ALL_WAITS"]
+        _compile_once(src, obj, safe)
+        asm = _device_asm(src, safe)
+        left = dma_sgpr_hazards(asm)
+        if left:
+            raise RuntimeError(f"{src.name}: direct-to-LDS loads read freshly written SGPRs:\n" + "\n".join(left[:5]))
+    bad = store_data_hazards(asm)
+    if bad:
+        raise RuntimeError(f"{src.name}: store data overwritten before the store read it:\n" + "\n".join(bad[:5]))
     return obj
 
 

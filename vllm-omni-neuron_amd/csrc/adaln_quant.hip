@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
           ov[j] = pack_bf16x2(h0 + bf16_lo(rv[j]), h1 + bf16_hi(rv[j]));
           xp[c][j] = ov[j];
         }
-        __builtin_amdgcn_raw_buffer_store_b128(ov, r_ro, lane * 16, c * 1024, 0);
+        store_b128_guarded(ov, r_ro, lane * 16, c * 1024);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xp[c][j] = 0u;
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
         u32x4 ov;
 #pragma unroll
         for (int j = 0; j < 4; ++j) ov[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
-        __builtin_amdgcn_raw_buffer_store_b128(ov, r_o, lane * 16, c * 1024, 0);
+        store_b128_guarded(ov, r_o, lane * 16, c * 1024);
       } else if (a.quant == WANMI_QUANT_MX) {
         // a 32-block is 4 consecutive lanes (col / 32 == c * 16 + lane / 4)
         int e = 0;

@@ -133,6 +133,19 @@ __device__ __forceinline__ void lds_dma_b128_hot(u32x4 rsrc, uint32_t voff, uint
   asm volatile(WANMI_DMA_HOT_NOP "buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
 }
 
+// A 16-byte buffer store followed by two wait states. A VALU write of a VGPR that holds the data of
+// a store wider than 64 bits must wait until the store has read it; the compiler's hazard check
+// has been seen to miss that on gfx950 (a register of the data was overwritten by the very next
+// instruction and some lanes stored the new value), so stores that the compiler may follow with a
+// write of their data registers go through this: no instruction moves between the store and the
+// nops. The build scans the generated code of every kernel for the pattern.
+__device__ __forceinline__ void store_b128_guarded(u32x4 v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 1" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Lane index recomputed on the spot (volatile, so not merged with earlier copies): code that runs
 // after a register-heavy loop derives its lane-dependent addresses from this instead of keeping
 // them live (and spilled) across the loop.
