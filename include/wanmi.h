@@ -110,6 +110,25 @@ int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, c
                                       per head (the reference's fused QKV kernel layout) */
 
 /*
+ * The fused [Q | K | V] projection in the attention's layouts: wanmi_mxfp8_gemm with the bf16
+ * epilogue on the columns [0, vt_col0) -- Q and K, into out (ldo >= vt_col0), with optional per-row
+ * partial sums of squares of the columns [0, sumsq_cols) in row_sumsq [M, vt_col0/128] as
+ * wanmi_mxfp8_gemm_rowsumsq writes them -- while the columns [vt_col0, N) -- V -- go to vt as V^T
+ * [(N - vt_col0)/128 heads][128][vt_ld] bf16 in the key order of wanmi_transpose_heads (inside each
+ * group of 16 keys: 0-3, 8-11, 4-7, 12-15), zero for tokens M .. vt_ld - 1. vt_col0 and N - vt_col0
+ * are multiples of 256, vt_ld >= M, vt_ld % 64 == 0. Two launches on `stream` (Q|K, then V, whose
+ * MFMAs take the token operand first so that four consecutive tokens of a feature are lane-local).
+ * Replaces the QKV kernel of row_mx_qkv_proj (vllm_omni_neuron/diffusion/quantization/
+ * row_mx_kernels.py:48-111, kernels/nkilib/core/qkv/qkv_cte.py:2725) together with the V transpose
+ * the reference's attention kernels do internally (ring_attention_const_max_fwd.py:1180-1220).
+ */
+int wanmi_mxfp8_gemm_qkv(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                         const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                         const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, void* out,
+                         int64_t ldo, float* row_sumsq, int64_t sumsq_cols, void* vt, int64_t vt_col0,
+                         int64_t vt_ld, void* stream);
+
+/*
  * Across-heads RMSNorm + optional 3D RoPE, in place on a bf16 [S, heads*128] slab (row stride ld
  * elements):  x = bf16(x * rrms * gamma), rrms = 1/sqrt(mean_row(x^2) + eps); then per pair (a, b)
  * of each head (rope_pairs selects which channels pair): (a, b) -> bf16(a cos - b sin),

@@ -76,13 +76,21 @@ class Failures(list):
 
 
 def snapshot_block(blk, w, h, temb, rope, cross):
-    """Run ``block_forward`` and keep a copy of every stage's output (the QKV buffer is normalized
-    in place right after its GEMM, so its snapshot is taken before that)."""
+    """Run ``block_forward`` and keep a copy of every stage's output (the Q|K buffer of the QKV GEMM
+    is normalized in place right after it, so its snapshot is taken before that)."""
     snap, live = {}, {}
+
+    def copy(r):
+        if isinstance(r, torch.Tensor):
+            return r.clone()
+        if isinstance(r, tuple) and all(isinstance(x, torch.Tensor) for x in r):
+            parts = [x.clone() for x in r]
+            return type(r)(*parts) if hasattr(r, "_fields") else tuple(parts)
+        return r
 
     def timer(name, fn):
         r = fn()
-        snap.setdefault(name, []).append(r.clone() if isinstance(r, torch.Tensor) else r)
+        snap.setdefault(name, []).append(copy(r))
         live.setdefault(name, []).append(r)
         return r
 
@@ -144,29 +152,30 @@ def check_block_rows(pkg, w, h, temb, rope, cross, rows, grid, eps=1e-6, fails=N
     np.testing.assert_array_equal(a1.scales[rd].cpu().numpy(), ref["scales"])
     pin_dq_and_product(a1.codes[rd], a1.scales[rd], w.qkv)
 
-    # QKV projection (before the in-place K norm)
-    qkv_pre = snap["gemm_qkv"][0]
+    # QKV projection: Q|K token-major (before the in-place K norm), V as V^T
+    qk_pre, vt = snap["gemm_qkv"][0]
     lin, absg = _gemm_rows(a1.codes, a1.scales, w.qkv, rd)
-    fails.within(qkv_pre[rd], lin, 2.0**-8 * lin.abs() + 2.0**-14 * absg, "qkv projection")
+    fails.within(qk_pre[rd], lin[:, : 2 * dim], 2.0**-8 * lin[:, : 2 * dim].abs() + 2.0**-14 * absg[:, : 2 * dim],
+                 "qkv projection (Q, K)")
+    v = _vt_to_tokens(vt, S)
+    fails.within(v[rd].reshape(-1, dim), lin[:, 2 * dim :], 2.0**-8 * lin[:, 2 * dim :].abs() + 2.0**-14 * absg[:, 2 * dim :],
+                 "qkv projection (V, written as V^T)")
+    assert not bool(_vt_to_tokens(vt, vt.shape[-1])[S:].any()), "V^T past the last token must be zero"
 
-    # K: across-heads RMSNorm + RoPE (in place), the key-norm bound, V^T
-    qkv_post = live["gemm_qkv"][0]
+    # K: across-heads RMSNorm + RoPE (in place) and the key-norm bound
+    qk_post = live["gemm_qkv"][0][0]
     cos_r, sin_r = rope[0][rd].cpu(), rope[1][rd].cpu()
     ic = torch.repeat_interleave(cos_r, 2, dim=-1)[None, :, None]
     isn = torch.repeat_interleave(sin_r, 2, dim=-1)[None, :, None]
-    k_pre = qkv_pre[rd, dim : 2 * dim].cpu()
+    k_pre = qk_pre[rd, dim:].cpu()
     k_ref = orope.rms_norm_across_heads(k_pre, w.norm_k.cpu(), eps).view(1, -1, heads, HEAD_DIM)
     k_ref = orope.apply_rotary_emb_wan(k_ref, ic, isn)[0].reshape(-1, dim)
-    fails.close(qkv_post[rd, dim : 2 * dim], k_ref, "K RMSNorm + RoPE")
-    k = qkv_post[:, dim : 2 * dim].view(S, heads, HEAD_DIM)
-    v = qkv_post[:, 2 * dim :].view(S, heads, HEAD_DIM)
+    fails.close(qk_post[rd, dim:], k_ref, "K RMSNorm + RoPE")
+    k = qk_post[:, dim:].view(S, heads, HEAD_DIM)
     kn = k.float().pow(2).sum(-1).sqrt().amax(0)
-    # the attention's bound: kmax over every key, from the kernel's own normalized K
-    vt = snap["v_transpose"][0][0]
-    assert torch.equal(_vt_to_tokens(vt, S), v), "V^T is not the transposed V"
 
     # self-attention: Q normalized + rotated on load; oracle prepares the same raw q rows
-    q_raw = qkv_pre[rd, :dim].cpu()
+    q_raw = qk_pre[rd, :dim].cpu()
     q_ref = orope.rms_norm_across_heads(q_raw, w.norm_q.cpu(), eps).view(1, -1, heads, HEAD_DIM)
     q_ref = orope.apply_rotary_emb_wan(q_ref, ic, isn)[0].to(dev)
     o1 = snap["self_attention"][0]

@@ -106,8 +106,13 @@ def run(pkg, dev):
 
     def timer(name, fn):
         r = fn()
-        # snapshot (the QKV buffer is normalized in place right after its GEMM) and keep the live object
-        snap.setdefault(name, []).append(r.clone() if isinstance(r, torch.Tensor) else r)
+        # snapshot (the Q|K buffer is normalized in place right after its GEMM) and keep the live object
+        if isinstance(r, tuple) and all(isinstance(x, torch.Tensor) for x in r):
+            parts = [x.clone() for x in r]
+            c = type(r)(*parts) if hasattr(r, "_fields") else tuple(parts)
+        else:
+            c = r.clone() if isinstance(r, torch.Tensor) else r
+        snap.setdefault(name, []).append(c)
         live.setdefault(name, []).append(r)
         return r
 
@@ -132,21 +137,29 @@ def test_block_stagewise(pkg, dev, run):
     ref = oadaln.adaln_quant(r["h"].float().numpy(), (1 + sc).numpy(), shift.numpy(), quant="mx")
     np.testing.assert_array_equal(_np8(a1.codes), ref["codes"])
     np.testing.assert_array_equal(a1.scales.cpu().numpy(), ref["scales"])
-    # QKV projection from the GPU's a1
-    qkv_pre = snap["gemm_qkv"][0].cpu()
-    _close(qkv_pre, oblock._lin(*_mx_np(a1), wq["qkv"], raw["qkv_b"]), "qkv projection")
+    # QKV projection from the GPU's a1: Q|K token-major, V written transposed (V^T)
+    qk_pre, vt = (t.cpu() for t in snap["gemm_qkv"][0])
+    order = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+    S_pad = vt.shape[-1]
+    slot_key = torch.tensor([16 * (i // 16) + order[i % 16] for i in range(S_pad)])
+    v_tok = torch.empty(S_pad, heads, D, dtype=torch.bfloat16)
+    v_tok[slot_key] = vt.permute(2, 0, 1)
+    assert not bool(v_tok[S:].float().any()), "V^T past the last token must be zero"
+    qkv_pre = torch.cat([qk_pre.float(), v_tok[:S].reshape(S, dim).float()], dim=1)
+    _close(qkv_pre, oblock._lin(*_mx_np(a1), wq["qkv"], raw["qkv_b"]), "qkv projection (V as V^T)")
     # Q/K RMSNorm + RoPE from the GPU's projection: K in place (its own pass), Q inside the attention
-    qkv_post = live["gemm_qkv"][0].cpu()
+    qkv_post = live["gemm_qkv"][0][0].cpu()
     refn = {}
     for part, gname in ((0, "norm_q"), (1, "norm_k")):
         x = qkv_pre[:, part * dim : (part + 1) * dim].to(torch.bfloat16)
         rn = orope.rms_norm_across_heads(x, raw[gname]).view(1, S, heads, D)
         refn[gname] = orope.apply_rotary_emb_wan(rn, r["cos"][None, :, None], r["sin"][None, :, None]).view(S, dim)
     _close(qkv_post[:, dim : 2 * dim], refn["norm_k"], "norm_k + RoPE")
-    assert torch.equal(qkv_post[:, :dim], qkv_pre[:, :dim].to(torch.bfloat16)), "Q must stay the raw projection"
+    assert torch.equal(qkv_post[:, :dim], qk_pre[:, :dim]), "Q must stay the raw projection"
     # self-attention from the GPU's raw q (normalized + rotated on load), k, v, against the oracle's
     # attention over the oracle-prepared q
-    k, v = (qkv_post[:, i * dim : (i + 1) * dim].view(S, heads, D) for i in (1, 2))
+    k = qkv_post[:, dim : 2 * dim].view(S, heads, D)
+    v = v_tok[:S]
     o1 = snap["self_attention"][0]
     _mx_close(o1, oblock._attend(refn["norm_q"].to(torch.bfloat16).view(S, heads, D), k, v, s),
               "self-attention with Q RMSNorm+RoPE on load (MX out)", 0.98)

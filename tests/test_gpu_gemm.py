@@ -215,3 +215,25 @@ def test_gemm_full_mlp_shapes_row_subset(pkg, dev):
     err = (y.double() - ref).abs()
     bound = 2.0**-8 * ref.abs() + (2.0**-7 * lin.abs() + 2.0**-14 * og.abs_gemm(*ops)) * gate_c.abs()
     assert bool((err <= bound + 1e-30).all())
+
+
+@pytest.mark.parametrize("M", [300, 1560, 4100])
+def test_qkv_projection_writes_v_transposed(pkg, dev, M):
+    """``mxfp8_qkv_linear``: the Q|K columns bit-identical to the plain GEMM's, the Q sums of squares
+    identical, and the V columns written as V^T in the attention's key order -- against
+    ``transpose_heads`` of the plain GEMM's V (zero past the last token) within one bf16 rounding (its MFMAs take the operands in the other order, so the fp32 accumulation may round
+    differently)."""
+    dim = 1024
+    xq, wq, _, _ = _operands(pkg, dev, M, 3 * dim, 640, seed=M)
+    ss_ref = torch.empty(M, 3 * dim // 128, device=dev)
+    full = pkg.mxfp8_linear(xq, wq, row_sumsq=ss_ref, sumsq_cols=dim)
+    ss = torch.full((M, 2 * dim // 128), float("nan"), device=dev)
+    qk, vt = pkg.row_mx_kernels.mxfp8_qkv_linear(xq, wq, vt_col0=2 * dim, row_sumsq=ss, sumsq_cols=dim)
+    assert qk.shape == (M, 2 * dim) and vt.shape == (dim // 128, 128, (M + 63) // 64 * 64)
+    assert torch.equal(qk, full[:, : 2 * dim])
+    vt_ref, _ = pkg.attention_ops.transpose_heads(full[:, 2 * dim :].view(M, dim // 128, 128))
+    d = (vt.float() - vt_ref.float()).abs()
+    assert bool((d <= 2.0**-8 * vt_ref.float().abs()).all()), float(d.max())
+    assert float((d > 0).float().mean()) < 1e-3
+    assert torch.equal(ss[:, : dim // 128], ss_ref[:, : dim // 128])
+    assert bool(torch.isnan(ss[:, dim // 128 :]).all())

@@ -12,7 +12,14 @@ The directory name contains dashes, so it is imported under the module name
 from . import _lib  # noqa: F401
 from .adaln_kernels import adaln_modulate  # noqa: F401
 from .common_types import MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401
-from .row_mx_kernels import MXWeight, mxfp8_linear, packed_weight_to_mx, quantize_weight_mx, row_mx_mlp  # noqa: F401
+from .row_mx_kernels import (  # noqa: F401
+    MXWeight,
+    mxfp8_linear,
+    mxfp8_qkv_linear,
+    packed_weight_to_mx,
+    quantize_weight_mx,
+    row_mx_mlp,
+)
 from . import rope  # noqa: F401
 from .rope import WanRotaryPosEmbed, rope_tables  # noqa: F401
 from . import attention_ops  # noqa: F401

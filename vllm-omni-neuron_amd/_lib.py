@@ -38,6 +38,8 @@ _SIGNATURES = {
     "wanmi_transpose_heads": [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "wanmi_head_max_norm": [_vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "wanmi_mxfp8_gemm_rowsumsq": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
+    "wanmi_mxfp8_gemm_qkv": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+                             _i64, _vp],
     "wanmi_attention_const_max": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _i64, _vp,

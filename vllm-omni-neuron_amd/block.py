@@ -5,8 +5,9 @@ wan2_2_transformer.py:1428-1513) with every projection in MXFP8 and attention in
 
     e = scale_shift_table + temb                     -> shift, scale, gate, c_shift, c_scale, c_gate
     a1 = MX(LN(h) * (1 + scale) + shift)              adaLN kernel
-    qkv = a1 @ Wqkv + b                               MXFP8 GEMM (+ per-row sums of q^2 per 128 columns)
-    k = RoPE(RMS_heads(k) g_k), max||k||; V^T         prep kernels
+    q, k, V^T = a1 @ Wqkv + b                         MXFP8 GEMM (+ per-row sums of q^2 per 128 columns;
+                                                      V written transposed for the attention)
+    k = RoPE(RMS_heads(k) g_k), max||k||              prep kernel
     o1 = MX(attention(RoPE(RMS_heads(q) g_q), k, v))  constant-max attention, Q prepared on load, MX out
     h1 = h + gate * (o1 @ Wo + b);  a2 = MX(LN_affine(h1))          GEMM (gated residual) + adaLN
     o2 = MX(attention(RMS_heads(a2 @ Wq2 + b) g_q2, K2, V2))    GEMM (+ sums of q2^2) + cross-attention
@@ -33,7 +34,7 @@ import torch
 
 from . import attention_ops as ops
 from .adaln_kernels import adaln_quant_2d
-from .row_mx_kernels import MXWeight, mxfp8_linear, quantize_weight_mx
+from .row_mx_kernels import MXWeight, mxfp8_linear, mxfp8_qkv_linear, quantize_weight_mx
 
 DIM, HEADS, HEAD_DIM, FFN = 5120, 40, 128, 13824
 
@@ -132,16 +133,15 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
     cos, sin = rope
 
     a1 = run("adaln", lambda: adaln_quant_2d(h, one_p_sc, shift, eps=eps, norm_type="layer_norm", quant="mx"))
-    # The Q rows' sums of squares come out of the QKV GEMM's epilogue (blocks 0 .. heads-1 of the
-    # 128-column blocks); the attention normalizes and rotates Q as it loads it. K is prepared in a
-    # pass of its own: the key-norm bound needs max ||k|| over all keys before the attention starts.
-    q_ss = torch.empty((S, 3 * dim // 128), dtype=torch.float32, device=h.device)
-    qkv = run("gemm_qkv", lambda: mxfp8_linear(a1, w.qkv, row_sumsq=q_ss, sumsq_cols=dim))
-    kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qkv[:, dim : 2 * dim], w.norm_k, cos=cos, sin=sin, eps=eps,
-                                                      want_max=True))
-    vt, _ = run("v_transpose", lambda: ops.transpose_heads(qkv[:, 2 * dim :].view(S, heads, HEAD_DIM)))
-    q = qkv[:, :dim].view(S, heads, HEAD_DIM)
-    k = qkv[:, dim : 2 * dim].view(S, heads, HEAD_DIM)
+    # The QKV GEMM writes Q and K token-major, V already transposed per head for the attention (V^T),
+    # and the Q rows' sums of squares per 128 columns; the attention normalizes and rotates Q as it
+    # loads it. K is prepared in a pass of its own: the key-norm bound needs max ||k|| over all keys
+    # before the attention starts.
+    q_ss = torch.empty((S, 2 * dim // 128), dtype=torch.float32, device=h.device)
+    qk, vt = run("gemm_qkv", lambda: mxfp8_qkv_linear(a1, w.qkv, vt_col0=2 * dim, row_sumsq=q_ss, sumsq_cols=dim))
+    kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qk[:, dim:], w.norm_k, cos=cos, sin=sin, eps=eps, want_max=True))
+    q = qk[:, :dim].view(S, heads, HEAD_DIM)
+    k = qk[:, dim:].view(S, heads, HEAD_DIM)
     o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX,
                                                          q_prep=ops.QPrep(q_ss, w.norm_q, cos, sin, eps)))
     h1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o, epilogue="gated_residual", residual=h, gate=gate))

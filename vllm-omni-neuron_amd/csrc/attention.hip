@@ -92,7 +92,13 @@ __device__ __forceinline__ f32x16 qk_half(const uint8_t* cK, int i, const bf16x8
 // P = exp2(S) for one half of shifted log2 logits, added to the lane's row sum and packed (bf16) as
 // the two 16-key B operands of O^T += V^T P^T. Accumulator register r of lane l holds key
 // 8 (r >> 2) + 4 (l >> 5) + (r & 3) of the half. kMask: keys at half positions >= `valid` get P = 0.
-template <bool kMask>
+// kSumBf16: the row sum adds the bf16 P that the P V product multiplies (two per v_dot2 against
+// (1, 1)), as the reference's [V | 1] column does (attention_const_max.py:454); otherwise it adds the
+// fp32 P. Measured against fp64 attention on MI355X (S = 32760, 3 heads): self-attention 2.958e-3
+// rms relative error either way, cross-attention over 512 keys 2.927e-3 (bf16 sum) vs 2.939e-3 (fp32
+// sum); the bf16 sum costs self-attention 1.3% (17.09 vs 16.87 ms) and cross-attention nothing, so
+// only the short-key instantiation uses it.
+template <bool kMask, bool kSumBf16>
 __device__ __forceinline__ void softmax_half(const f32x16& s, int hq, int valid, float& lsum, bf16x8 (&pf)[2]) {
 #pragma clang fp contract(off)
   float p[16];
@@ -101,15 +107,22 @@ __device__ __forceinline__ void softmax_half(const f32x16& s, int hq, int valid,
     float x = __builtin_amdgcn_exp2f(s[r]);
     if constexpr (kMask) x = (r >> 2) * 8 + hq * 4 + (r & 3) < valid ? x : 0.0f;
     p[r] = x;
-    lsum = lsum + x;
+    if constexpr (!kSumBf16) lsum = lsum + x;
   }
+  [[maybe_unused]] const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+  [[maybe_unused]] float part[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(p[8 * u + 2 * j], p[8 * u + 2 * j + 1]);
+    for (int j = 0; j < 4; ++j) {
+      w[j] = pack_bf16x2(p[8 * u + 2 * j], p[8 * u + 2 * j + 1]);
+      if constexpr (kSumBf16)
+        part[u] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[j]), ones, part[u], false);
+    }
     pf[u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
   }
+  if constexpr (kSumBf16) lsum = lsum + (part[0] + part[1]);
 }
 
 // O^T += V^T P^T for one 32-key half (16-key groups 2 i, 2 i + 1 of the LDS tile): 8 MFMAs in four
@@ -131,19 +144,19 @@ __device__ __forceinline__ void pv_half(const uint8_t* cV, int i, const bf16x8 (
 // One step of the per-wave software pipeline over 32-key halves: the QK^T MFMAs of half h (K from
 // cK, half i_cur) are independent of the softmax of half h-1 (s_prev), so the two streams interleave
 // on the matrix and vector pipes; then half h-1's P V MFMAs (V from cV, half i_prev).
-template <bool kMask>
+template <bool kMask, bool kSumBf16>
 __device__ __forceinline__ void pipeline_step(const uint8_t* cK, int i_cur, const uint8_t* cV, int i_prev,
                                               const bf16x8 (&qf)[8], const f32x16& negc, f32x16& s_prev,
                                               f32x16 (&acc_o)[4], float& lsum, int col, int hq, int valid_prev) {
   const f32x16 s_cur = qk_half(cK, i_cur, qf, negc, col, hq);
   bf16x8 pf[2];
-  softmax_half<kMask>(s_prev, hq, valid_prev, lsum, pf);
+  softmax_half<kMask, kSumBf16>(s_prev, hq, valid_prev, lsum, pf);
   pv_half(cV, i_prev, pf, acc_o, col, hq);
   s_prev = s_cur;
 }
 
 // kShortKV: a separate instantiation for short key sequences (cross-attention over text tokens) so
-// the two uses can be specialized and profiled apart.
+// the two uses can be specialized and profiled apart; it sums the bf16 P (see softmax_half).
 // kRebaseK: one head of K spans more than 2 GiB (the fused QKV layout, row stride 15360, at 720p), so
 // the K descriptor is rebuilt at each tile's first key; otherwise one descriptor covers the head and
 // the tile's offset travels in the wave-uniform soffset.
@@ -319,9 +332,9 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   f32x16 s_prev = qk_half(sK[0], 0, qf, negc, col, hq);
   const int sk_rem = (int)(a.Sk - (int64_t)(ntiles - 1) * BKV);  // keys in the last tile (1..64)
   if (ntiles == 1)
-    pipeline_step<true>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
+    pipeline_step<true, kShortKV>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
   else
-    pipeline_step<false>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<false, kShortKV>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
   // Tile t of the steady state (1 <= t < ntiles - 1): outstanding loads are tiles t and t+1 (four
   // per wave each); wait for tile t, publish it, refill tile t-2's slot with tile t+2, then the two
   // pipeline steps of t (`slot` = t % kStages).
@@ -330,8 +343,8 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     __syncthreads();
     if (t + 2 < ntiles) issue_tile(t + 2);
     const int prev = (slot + kStages - 1) % kStages;
-    pipeline_step<false>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
-    pipeline_step<false>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<false, kShortKV>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<false, kShortKV>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
   };
   for (int t = 1; t < ntiles - 1; ++t) steady_tile(t, t % kStages);
   if (ntiles > 1) {
@@ -339,12 +352,12 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
     const uint8_t* kc = sK[tl % kStages];
-    pipeline_step<false>(kc, 0, sV[(tl - 1) % kStages], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
-    pipeline_step<true>(kc, 1, sV[tl % kStages], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
+    pipeline_step<false, kShortKV>(kc, 0, sV[(tl - 1) % kStages], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    pipeline_step<true, kShortKV>(kc, 1, sV[tl % kStages], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
   }
   {  // drain: softmax and P V of the last half
     bf16x8 pf[2];
-    softmax_half<true>(s_prev, hq, sk_rem - 32, lsum, pf);
+    softmax_half<true, kShortKV>(s_prev, hq, sk_rem - 32, lsum, pf);
     pv_half(sV[(ntiles - 1) % kStages], 1, pf, acc_o, col, hq);
   }
 

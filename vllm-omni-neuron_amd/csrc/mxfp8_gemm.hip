@@ -72,6 +72,9 @@ struct GemmArgs {
   uint8_t* out_scales;      // [M, N/32]
   float* row_sumsq;         // [M, N/128]: sum of squares of the bf16 outputs per 128-column block, or null
   int64_t sumsq_cols;       // blocks of columns [0, sumsq_cols) are summed
+  int64_t sumsq_ld;         // row stride of row_sumsq in floats
+  uint16_t* vt;             // V^T epilogue: [N/128][128][vt_ld] bf16
+  int64_t vt_ld;
   int64_t M, N, K, lda, ldo;
   int tiles_m, tiles_n;
 };
@@ -137,15 +140,24 @@ __device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* 
   }
 }
 
+// One MFMA of weight fragment i against token fragment j. kSwap puts the tokens in the A operand,
+// so the accumulator is transposed: lane l holds feature 32 i + (l & 31) and tokens
+// 32 j + 8 g + 4 (l >> 5) + q (the V^T epilogue's layout); otherwise features along the registers.
+template <bool kSwap>
+__device__ __forceinline__ f32x16 mfma_tile(const i32x8& w, const i32x8& a, const f32x16& c, int ws, int as) {
+  if constexpr (kSwap)
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, w, c, 0, 0, 0, as, 0, ws);
+  else
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, ws, 0, as);
+}
+
 // MFMAs of weight-row fragments [I0, I1) against all four token fragments.
-template <int I0, int I1>
+template <int I0, int I1, bool kSwap = false>
 __device__ __forceinline__ void mfma_rows(const SliceOperands& op, f32x16 (&acc)[4][4]) {
 #pragma unroll
   for (int i = I0; i < I1; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op.w[i], op.a[j], acc[i][j], 0, 0, 0, op.ws[i], 0,
-                                                                   op.as[j]);
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma_tile<kSwap>(op.w[i], op.a[j], acc[i][j], op.ws[i], op.as[j]);
 }
 
 // Per-tile buffer resources of one wave's direct-to-LDS loads.
@@ -242,17 +254,17 @@ __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& 
 // would hold the wave at the texture unit's input queue (each moves 1 KiB) while its matrix pipe runs
 // dry. The scheduling barriers keep the compiler from regrouping them (it otherwise moves MFMAs
 // across the stage's barrier and clusters the reads).
-template <int I>
+template <int I, bool kSwap>
 __device__ __forceinline__ void phase_a_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
                                             const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
                                             int r32, uint32_t sl) {
   read_slice<I, I + 1>(base, sc, q, s, nxt, wn, wm, h, r32, sl);
   __builtin_amdgcn_sched_barrier(0);
-  mfma_rows<I, I + 1>(cur, acc);
+  mfma_rows<I, I + 1, kSwap>(cur, acc);
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int I>
+template <int I, bool kSwap>
 __device__ __forceinline__ void phase_b_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
                                             const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
                                             int r32, uint32_t sl, const GemmArgs& g, const TileLoads& t,
@@ -261,8 +273,7 @@ __device__ __forceinline__ void phase_b_row(const uint8_t* base, const uint32_t*
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    acc[I][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.w[I], cur.a[j], acc[I][j], 0, 0, 0, cur.ws[I], 0,
-                                                                 cur.as[j]);
+    acc[I][j] = mfma_tile<kSwap>(cur.w[I], cur.a[j], acc[I][j], cur.ws[I], cur.as[j]);
     if (j == 0 || j == 2) code_dma_pair<true>(g, t, dl, kt, buf, wave, 2 * I + (j >> 1), valid);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -464,7 +475,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
           const float other = __shfl_xor(ss, 32, 64);
           const float tot = h == 0 ? ss + other : other + ss;
           const int m = m0 + wm * 128 + j * 32 + r32;
-          if (h == 0 && m < (int)g.M) g.row_sumsq[(uint32_t)m * (uint32_t)(g.N / 128) + (uint32_t)(nw / 128)] = tot;
+          if (h == 0 && m < (int)g.M) g.row_sumsq[(uint32_t)m * (uint32_t)g.sumsq_ld + (uint32_t)(nw / 128)] = tot;
         }
       }
       if constexpr (EPI == WANMI_EPI_GELU_MX) {
@@ -541,12 +552,95 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
   }
 }
 
+// V^T epilogue: the V columns of the fused QKV projection, written in the attention kernel's V^T
+// layout. It runs on the transposed accumulator (kSwap: lane l holds feature 32 i + (l & 31) and
+// tokens 32 j + 8 g + 4 (l >> 5) + q), so four consecutive tokens of one feature are lane-local. The
+// wave's 128 features are one head (the V columns start at a multiple of 256); its tokens become
+// columns of the head's 128 rows [d][vt_ld]. Inside each group of 16 the keys are stored in the order
+// (0-3, 8-11, 4-7, 12-15) -- the order in which the attention's P registers hand keys to its P V
+// MFMA -- so the 4 tokens 8 g + 4 h + q of a lane land in storage slots 4 (2 h + (g & 1)) + q of their
+// group: one 8-byte LDS write. Tokens >= M are written as zero. Each half of 64 tokens is staged as
+// [128 d][64 slots] bf16 in the wave's LDS area, 16-byte chunks XOR-swizzled by (d >> 1) & 7 so that
+// the writes of 32 rows spread over the banks, then stored as whole 128-byte row segments, 8 lanes
+// per row; segments at or past vt_ld are dropped.
+constexpr int kEpiVt = 100;  // internal epilogue id (wanmi_mxfp8_gemm_qkv only)
+
+__device__ __forceinline__ int vt_chunk(int d, int c16) { return d * 128 + ((c16 ^ ((d >> 1) & 7)) << 4); }
+
+template <bool kScaled>
+__device__ __forceinline__ void epilogue_vt(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec,
+                                            uint8_t* stage, int m0, int n0, int wm, int wn) {
+#pragma clang fp contract(off)
+  const int lane = fresh_lane_id();
+  const int h = lane >> 5, r32 = lane & 31;
+  // this lane's feature of each 32-feature fragment: bias and column scale
+  float fb[4], fc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    fb[i] = vec[wn * 128 + i * 32 + r32];
+    fc[i] = kScaled ? vec[256 + wn * 128 + i * 32 + r32] : 1.0f;
+  }
+  const int64_t vrow0 = (int64_t)(n0 + wn * 128);  // first V^T row of the wave (head * 128), W rows offset
+  const auto vrsrc = rows_rsrc(g.vt + vrow0 * g.vt_ld, 128, (uint32_t)g.vt_ld * 2);
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * hf + jj;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int tok0 = wm * 128 + j * 32 + 8 * gq + 4 * h;  // first of the 4 tokens, within the tile
+        float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (kScaled) {
+          const float4 r4 = *reinterpret_cast<const float4*>(vec + 768 + tok0);
+          rs[0] = r4.x, rs[1] = r4.y, rs[2] = r4.z, rs[3] = r4.w;
+        }
+        const int live = (int)g.M - (m0 + tok0);  // tokens q < live are inside M
+        const int c16 = 2 * (2 * jj + (gq >> 1)) + h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float y[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float a = acc[i][j][gq * 4 + q];
+            const float v = kScaled ? (a * rs[q]) * fc[i] + fb[i] : a + fb[i];
+            y[q] = q < live ? v : 0.0f;
+          }
+          const int d = i * 32 + r32;
+          *reinterpret_cast<uint2*>(stage + vt_chunk(d, c16) + (gq & 1) * 8) =
+              make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        }
+      }
+    }
+    const int mbase = m0 + wm * 128 + hf * 64;
+    if (hf == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // loads before stores, as in epilogue()
+    const int chunk = lane & 7;
+    const uint32_t col_bytes = (uint32_t)(mbase + chunk * 8) * 2;
+    const bool in_row = mbase + chunk * 8 < (int)g.vt_ld;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {  // two batches of 8 reads, then 8 stores
+      uint4 dv[8];
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        dv[it] = *reinterpret_cast<const uint4*>(stage + vt_chunk((b * 8 + it) * 8 + (lane >> 3), chunk));
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const uint32_t d = (uint32_t)((b * 8 + it) * 8 + (lane >> 3));
+        // an offset past the resource's extent drops the store (segments at or past vt_ld)
+        const uint32_t off = in_row ? d * (uint32_t)g.vt_ld * 2 + col_bytes : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{dv[it].x, dv[it].y, dv[it].z, dv[it].w}, vrsrc, (int)off, 0, 0);
+      }
+    }
+  }
+}
+
 // kPipelined: the pipelined main loop (K a multiple of 512: whole scale groups, stage pairs);
 // otherwise a simple double-buffered loop that issues the next stage's loads after all reads of the
 // current one.
 template <bool kPipelined, int EPI>
 __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
+  constexpr bool kSwap = EPI == kEpiVt;  // the V^T epilogue wants the transposed accumulator
   __shared__ __attribute__((aligned(16))) uint8_t smem0[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t smem1[kStageBytes];
   __shared__ __attribute__((aligned(16))) uint32_t ssc[2][2 * 256 * 4];  // scale groups, double-buffered
@@ -614,9 +708,9 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
         SliceOperands op;
         const uint32_t sl = scale_lane_offset();
         read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32, sl);
-        mfma_rows<0, 4>(op, acc);
+        mfma_rows<0, 4, kSwap>(op, acc);
         read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32, sl);
-        mfma_rows<0, 4>(op, acc);
+        mfma_rows<0, 4, kSwap>(op, acc);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
@@ -635,20 +729,20 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
       // in the final phase B is dead.
 #define WANMI_GEMM_STAGE(S, CUR, OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                     \
   do {                                                                                             \
-    phase_a_row<0>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<1>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<2>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<3>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<0, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<1, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<2, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
+    phase_a_row<3, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
     __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                   \
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));                                                     \
     __syncthreads();                                                                               \
     const bool more_ = (S) + 2 < KT;                                                               \
     const int ktn_ = more_ ? (S) + 2 : 0;                                                          \
     if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
-    phase_b_row<0>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<1>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<2>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<3>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<0, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<1, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<2, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
+    phase_b_row<3, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
   } while (0)
 
       // per-lane load and scale-read offsets, held through the k loop and dead after it
@@ -678,7 +772,10 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     {
       uint8_t* stage = smem1 + wave * kStageWave;
       const bool scaled = g.row_scale || g.col_scale;
-      if constexpr (EPI == WANMI_EPI_BF16) {
+      if constexpr (EPI == kEpiVt) {
+        if (scaled) epilogue_vt<true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+        else epilogue_vt<false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+      } else if constexpr (EPI == WANMI_EPI_BF16) {
         if (g.row_sumsq) {
           if (scaled) epilogue<EPI, true, true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
           else epilogue<EPI, false, true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
@@ -707,6 +804,7 @@ static void launch_gemm(int epilogue, dim3 grid, hipStream_t stream, const GemmA
     case WANMI_EPI_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_BF16>), grid, dim3(256), 0, stream, g); break;
     case WANMI_EPI_GELU_MX: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_MX>), grid, dim3(256), 0, stream, g); break;
     case WANMI_EPI_GELU_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_BF16>), grid, dim3(256), 0, stream, g); break;
+    case kEpiVt: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, kEpiVt>), grid, dim3(256), 0, stream, g); break;
     default: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GATED_RESIDUAL>), grid, dim3(256), 0, stream, g); break;
   }
 }
@@ -717,21 +815,23 @@ namespace wanmi {
 static int gemm_impl(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes, const uint8_t* w_scales,
                      const float* row_scale, const float* col_scale, const float* bias, int64_t M, int64_t N,
                      int64_t K, int64_t lda, int epilogue, void* out, int64_t ldo, uint8_t* out_scales,
-                     const void* residual, const float* gate, float* row_sumsq, int64_t sumsq_cols, void* stream) {
+                     const void* residual, const float* gate, float* row_sumsq, int64_t sumsq_cols, int64_t sumsq_ld,
+                     void* vt, int64_t vt_ld, void* stream) {
   WANMI_REQUIRE(M >= 0 && N > 0 && K > 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: bad sizes M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
   WANMI_REQUIRE(N % TN == 0, WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: N=%lld must be a multiple of %d",
                 (long long)N, TN);
   WANMI_REQUIRE(K % BK == 0, WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: K=%lld must be a multiple of %d",
                 (long long)K, BK);
-  WANMI_REQUIRE(epilogue >= WANMI_EPI_BF16 && epilogue <= WANMI_EPI_GATED_RESIDUAL, WANMI_ERR_ARG,
-                "wanmi_mxfp8_gemm: unknown epilogue %d", epilogue);
+  WANMI_REQUIRE((epilogue >= WANMI_EPI_BF16 && epilogue <= WANMI_EPI_GATED_RESIDUAL) || epilogue == kEpiVt,
+                WANMI_ERR_ARG, "wanmi_mxfp8_gemm: unknown epilogue %d", epilogue);
   WANMI_REQUIRE(lda >= K && lda % 16 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: lda=%lld must be >= K and a multiple of 16",
                 (long long)lda);
-  WANMI_REQUIRE(ldo >= N && ldo % 16 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm: ldo=%lld must be >= N and a multiple of 16",
-                (long long)ldo);
+  const bool to_vt = epilogue == kEpiVt;
+  WANMI_REQUIRE(to_vt || (ldo >= N && ldo % 16 == 0), WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm: ldo=%lld must be >= N and a multiple of 16", (long long)ldo);
   if (M == 0) return WANMI_OK;
-  WANMI_REQUIRE(a_codes && a_scales && w_codes && w_scales && out, WANMI_ERR_ARG,
+  WANMI_REQUIRE(a_codes && a_scales && w_codes && w_scales && (to_vt ? vt != nullptr : out != nullptr), WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm: null operand");
   WANMI_REQUIRE(epilogue != WANMI_EPI_GELU_MX || out_scales, WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm: GELU_MX epilogue needs out_scales");
@@ -742,18 +842,21 @@ static int gemm_impl(const uint8_t* a_codes, const uint8_t* a_scales, const uint
                     ((uintptr_t)out % 16) == 0 && (!out_scales || ((uintptr_t)out_scales % 4) == 0) &&
                     (!bias || ((uintptr_t)bias % 16) == 0) &&
                     (!col_scale || ((uintptr_t)col_scale % 16) == 0) &&
-                    (!gate || ((uintptr_t)gate % 16) == 0) && (!residual || ((uintptr_t)residual % 16) == 0),
+                    (!gate || ((uintptr_t)gate % 16) == 0) && (!residual || ((uintptr_t)residual % 16) == 0) &&
+                    ((uintptr_t)vt % 16) == 0,
                 WANMI_ERR_ARG, "wanmi_mxfp8_gemm: misaligned operand");
   const int64_t tiles = (N / TN) * ((M + TM - 1) / TM);
   WANMI_REQUIRE(tiles < (1LL << 31), WANMI_ERR_ARG, "wanmi_mxfp8_gemm: problem too large");
-  WANMI_REQUIRE(M * ldo < (1LL << 32) && M < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+  WANMI_REQUIRE(to_vt || (M * ldo < (1LL << 32) && M < (1LL << 31)), WANMI_ERR_UNSUPPORTED,
                 "wanmi_mxfp8_gemm: M=%lld x ldo=%lld output elements exceed 32-bit offsets", (long long)M, (long long)ldo);
+  WANMI_REQUIRE(!to_vt || (vt_ld >= M && vt_ld % 64 == 0 && 128 * vt_ld * 2 < (1LL << 31)), WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm: vt_ld=%lld must be >= M, a multiple of 64 and below 2^23", (long long)vt_ld);
   // per-tile buffer offsets are 32-bit; this also keeps K and lda below 2^23 for the 24-bit
   // multiplies of the load offsets
   WANMI_REQUIRE(TN * K < (1LL << 31) && TM * lda < (1LL << 31), WANMI_ERR_UNSUPPORTED,
                 "wanmi_mxfp8_gemm: K=%lld / lda=%lld too large", (long long)K, (long long)lda);
   // the epilogue's store resources span 64 output rows with 32-bit offsets
-  WANMI_REQUIRE(ldo < (1LL << 22), WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: ldo=%lld too large", (long long)ldo);
+  WANMI_REQUIRE(to_vt || ldo < (1LL << 22), WANMI_ERR_UNSUPPORTED, "wanmi_mxfp8_gemm: ldo=%lld too large", (long long)ldo);
 
   GemmArgs g;
   g.a = a_codes;
@@ -769,6 +872,9 @@ static int gemm_impl(const uint8_t* a_codes, const uint8_t* a_scales, const uint
   g.out_scales = out_scales;
   g.row_sumsq = row_sumsq;
   g.sumsq_cols = row_sumsq ? sumsq_cols : 0;
+  g.sumsq_ld = sumsq_ld;
+  g.vt = static_cast<uint16_t*>(vt);
+  g.vt_ld = vt_ld;
   g.M = M;
   g.N = N;
   g.K = K;
@@ -794,8 +900,10 @@ extern "C" int wanmi_mxfp8_gemm(const uint8_t* a_codes, const uint8_t* a_scales,
                                 int epilogue, void* out, int64_t ldo, uint8_t* out_scales,
                                 const void* residual, const float* gate, void* stream) {
   wanmi::clear_error();
+  WANMI_REQUIRE(epilogue >= WANMI_EPI_BF16 && epilogue <= WANMI_EPI_GATED_RESIDUAL, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm: unknown epilogue %d", epilogue);
   return wanmi::gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, N, K, lda, epilogue,
-                          out, ldo, out_scales, residual, gate, nullptr, 0, stream);
+                          out, ldo, out_scales, residual, gate, nullptr, 0, 0, nullptr, 0, stream);
 }
 
 extern "C" int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
@@ -809,5 +917,31 @@ extern "C" int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* 
   WANMI_REQUIRE(sumsq_cols >= 0 && sumsq_cols <= N && sumsq_cols % 128 == 0, WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm_rowsumsq: sumsq_cols=%lld must be a multiple of 128 in [0, N]", (long long)sumsq_cols);
   return gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, N, K, lda, WANMI_EPI_BF16, out,
-                   ldo, nullptr, nullptr, nullptr, row_sumsq, sumsq_cols, stream);
+                   ldo, nullptr, nullptr, nullptr, row_sumsq, sumsq_cols, N / 128, nullptr, 0, stream);
+}
+
+extern "C" int wanmi_mxfp8_gemm_qkv(const uint8_t* a_codes, const uint8_t* a_scales, const uint8_t* w_codes,
+                                    const uint8_t* w_scales, const float* row_scale, const float* col_scale,
+                                    const float* bias, int64_t M, int64_t N, int64_t K, int64_t lda, void* out,
+                                    int64_t ldo, float* row_sumsq, int64_t sumsq_cols, void* vt, int64_t vt_col0,
+                                    int64_t vt_ld, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(vt && ((uintptr_t)vt % 16) == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm_qkv: vt must be a 16-byte aligned pointer");
+  WANMI_REQUIRE(vt_col0 > 0 && vt_col0 < N && vt_col0 % TN == 0 && (N - vt_col0) % TN == 0, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_qkv: vt_col0=%lld must be a multiple of %d inside (0, N)", (long long)vt_col0, TN);
+  WANMI_REQUIRE(!row_sumsq || ((uintptr_t)row_sumsq % 4) == 0, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_qkv: row_sumsq must be 4-byte aligned");
+  WANMI_REQUIRE(sumsq_cols >= 0 && sumsq_cols <= vt_col0 && sumsq_cols % 128 == 0, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_qkv: sumsq_cols=%lld must be a multiple of 128 in [0, vt_col0]", (long long)sumsq_cols);
+  WANMI_REQUIRE(K % 32 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm_qkv: K=%lld must be a multiple of 32", (long long)K);
+  // Q | K: the plain bf16 epilogue (with the Q partial sums) on the weight rows [0, vt_col0)
+  int st = gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, vt_col0, K, lda,
+                     WANMI_EPI_BF16, out, ldo, nullptr, nullptr, nullptr, row_sumsq, row_sumsq ? sumsq_cols : 0,
+                     vt_col0 / 128, nullptr, 0, stream);
+  if (st != WANMI_OK) return st;
+  // V: the weight rows [vt_col0, N), transposed accumulator, V^T epilogue
+  return gemm_impl(a_codes, a_scales, w_codes + vt_col0 * K, w_scales + vt_col0 * (K / 32), row_scale,
+                   col_scale ? col_scale + vt_col0 : nullptr, bias ? bias + vt_col0 : nullptr, M, N - vt_col0, K, lda,
+                   kEpiVt, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0, 0, vt, vt_ld, stream);
 }

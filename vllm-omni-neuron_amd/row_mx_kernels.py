@@ -239,6 +239,41 @@ def mxfp8_linear(
     return out.reshape(*lead, N)
 
 
+def mxfp8_qkv_linear(x, weight: MXWeight, *, vt_col0: int, row_sumsq: torch.Tensor | None = None,
+                     sumsq_cols: int = 0, head_dim: int = 128):
+    """The fused ``[Q | K | V]`` projection in the attention's layouts: returns ``(qk, vt)`` with
+    ``qk`` bf16 ``[M, vt_col0]`` (the columns before ``vt_col0``, token-major) and ``vt`` bf16
+    ``[(N - vt_col0) / 128, 128, S_pad]`` (the V columns transposed per head into the attention
+    kernel's key order, S_pad = M rounded up to 64, zero past M). ``row_sumsq``: fp32
+    ``[M, vt_col0/128]`` receiving the per-128-column sums of squares of the bf16 outputs for the
+    blocks of ``[0, sumsq_cols)``, as in :func:`mxfp8_linear`."""
+    lib = _lib.load()
+    _check_weight(weight)
+    codes, scales, row_scale, lead = _as_mx_2d(x)
+    M, K = codes.shape
+    N = weight.out_features
+    if weight.in_features != K:
+        raise ValueError(f"activation K={K} does not match weight K={weight.in_features}")
+    if vt_col0 <= 0 or vt_col0 >= N or vt_col0 % 256 or (N - vt_col0) % 256:
+        raise ValueError(f"vt_col0={vt_col0} and N - vt_col0 must be multiples of 256 (N={N})")
+    if row_sumsq is not None:
+        _lib.expect(row_sumsq, "row_sumsq", dtype=torch.float32, shape=(M, vt_col0 // 128))
+    _lib.require_gpu(codes, scales, row_scale, weight.codes, weight.scales, weight.col_scale, weight.bias, row_sumsq,
+                     what="mxfp8_qkv_linear")
+    dev = codes.device
+    s_pad = (max(M, 1) + 63) // 64 * 64
+    qk = torch.empty((M, vt_col0), dtype=torch.bfloat16, device=dev)
+    vt = torch.empty(((N - vt_col0) // head_dim, head_dim, s_pad), dtype=torch.bfloat16, device=dev)
+    status = lib.wanmi_mxfp8_gemm_qkv(
+        _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(weight.codes), _lib.ptr(weight.scales), _lib.ptr(row_scale),
+        _lib.ptr(weight.col_scale), _lib.ptr(weight.bias), M, N, K, codes.stride(0), _lib.ptr(qk), qk.stride(0),
+        _lib.ptr(row_sumsq), int(sumsq_cols) if row_sumsq is not None else 0, _lib.ptr(vt), vt_col0, s_pad,
+        _lib.stream_of(codes),
+    )
+    _lib.check(status, "wanmi_mxfp8_gemm_qkv")
+    return qk.reshape(*lead, vt_col0), vt
+
+
 def row_mx_mlp(
     packed_hidden,
     up_weight: MXWeight,
