@@ -40,6 +40,7 @@ def parse():
     p.add_argument("--grid", type=str, default="21,30,52", help="latent patch grid F,H,W")
     p.add_argument("--blocks", type=int, default=40)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-720p", action="store_true", help="skip the 720p (21x45x80) single-block timing")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="also run one 256 MiB device copy, the known-size reference for HBM counters")
     return p.parse_args()
@@ -154,6 +155,43 @@ def cpu_baseline(S_full, blocks):
     }
 
 
+def block_720p(pkg, w, cross, temb, dev, reps=3):
+    """One block at the 720p step's length (21x45x80 = 75600 tokens; block 0's weights and text K/V),
+    timed after the main metric: mean of `reps` launches after one warm-up, per-kernel HIP events
+    from one more; the 40-block step is estimated as 40 x the block."""
+    blk = pkg.block
+    grid = (21, 45, 80)
+    S7 = grid[0] * grid[1] * grid[2]
+    gen = torch.Generator(device=dev).manual_seed(720)
+    h = torch.randn(S7, DIM, device=dev, generator=gen).to(torch.bfloat16)
+    rope = pkg.rope_tables(grid, device=dev)
+    mod = blk.modulation(w.scale_shift_table[None], temb)[0]
+    blk.block_forward(w, h, temb, rope, cross, mod=mod)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        out = blk.block_forward(w, h, temb, rope, cross, mod=mod)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    timer = KernelTimer()
+    timer.active = True
+    blk.block_forward(w, h, temb, rope, cross, mod=mod, timer=timer)
+    torch.cuda.synchronize()
+    comp = {k: round(sum(v), 3) for k, v in sorted(timer.summary().items())}
+    attn_ms = comp["self_attention"]
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("non-finite 720p block output")
+    return {
+        "workload": "one Wan2.2-A14B block at 720p: 21x45x80 = 75600 tokens, 512 text tokens",
+        "seq_len": S7, "ms_per_block": round(ms, 2), "ms_per_step_estimate_40_blocks": round(40 * ms, 1),
+        "self_attention_tflops": round(4.0 * S7 * S7 * HEAD_DIM * HEADS / attn_ms / 1e9, 1),
+        "gemm_tflops": round(gemm_flops(S7) / sum(v for k, v in comp.items() if k.startswith("gemm_")) / 1e9, 1),
+        "components_ms": comp,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -174,6 +212,7 @@ def main():
     ctx = torch.randn(TXT, DIM, device=dev, generator=gen).to(torch.bfloat16)
     rope = pkg.rope_tables(grid, device=dev)  # built once per generation (not timed)
     crosses = [blk.project_cross_kv(w, ctx) for w in blocks]
+    tables = torch.stack([w.scale_shift_table for w in blocks])
     torch.cuda.synchronize()
 
     if args.pmc_calibration:
@@ -185,14 +224,14 @@ def main():
 
     timer = KernelTimer()
     for _ in range(args.warmup):
-        blk.dit_forward(blocks, h0, temb, rope, crosses)
+        blk.dit_forward(blocks, h0, temb, rope, crosses, tables=tables)
     torch.cuda.synchronize()
 
     timer.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out = blk.dit_forward(blocks, h0, temb, rope, crosses, timer=timer)
+        out = blk.dit_forward(blocks, h0, temb, rope, crosses, timer=timer, tables=tables)
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1000.0
     timer.active = False
@@ -254,6 +293,8 @@ def main():
             "traffic": load_traffic(S),
         },
     }
+    if not args.no_720p:
+        result["p720"] = block_720p(pkg, blocks[0], crosses[0], temb, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(S, args.blocks)
     print(json.dumps(result), flush=True)

@@ -7,7 +7,7 @@ fixed definition of the row statistics so that a GPU result can be compared bit 
     Summation order (fp32): the row is cut into chunks of 512 columns; "lane" l (0..63) owns
     columns c*512 + 8l .. 8l+7 of every chunk c and adds its values sequentially (chunk by chunk,
     column order inside a chunk); the 64 lane sums then combine in an xor butterfly with offsets
-    32, 16, 8, 4, 2, 1 (v_l <- v_l + v_(l^o)).
+    1, 2, 4, 8, 16, 32 (v_l <- v_l + v_(l^o)).
     LayerNorm (two-pass): mu = S1 / H,  S1 = sum x
                           var = S2 / H, S2 = sum fl(fl(x - mu)^2),  rstd = fp32(1/sqrt(fp64(var) + eps))
                           xh = fl32(fl32(x - mu) * rstd)
@@ -47,7 +47,7 @@ def _ordered_sum(terms: np.ndarray) -> np.ndarray:
     for i in range(terms.shape[2]):
         acc = (acc + terms[:, :, i]).astype(np.float32)
     lanes = np.arange(64)
-    for o in (32, 16, 8, 4, 2, 1):
+    for o in (1, 2, 4, 8, 16, 32):
         acc = (acc + acc[:, lanes ^ o]).astype(np.float32)
     return acc[:, :1]
 

@@ -119,17 +119,28 @@ def _ones(n: int, device) -> torch.Tensor:
     return _ONES[key]
 
 
+def modulation(tables: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+    """``e = scale_shift_table + temb`` (wan2_2_transformer.py:1454-1456) for a stack of blocks'
+    tables ``[B, 6, DIM]`` at once, as the rows the block uses: fp32 ``[B, 6, DIM]`` holding
+    shift, 1 + scale, gate, c_shift, 1 + c_scale, c_gate (each row contiguous)."""
+    e = tables.float() + temb.reshape(1, 6, -1).float()
+    e[:, 1] += 1.0
+    e[:, 4] += 1.0
+    return e
+
+
 def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cross: CrossKV,
-                  eps: float = 1e-6, timer=None) -> torch.Tensor:
+                  eps: float = 1e-6, timer=None, mod: torch.Tensor | None = None) -> torch.Tensor:
     """One block on ``h`` bf16 ``[S, DIM]``; ``temb`` ``[6, DIM]`` (or ``[1, 6, DIM]``); ``rope`` is
-    ``(cos, sin)`` pair tables ``[S, 64]``. ``timer(name, fn)`` optionally wraps each kernel launch."""
+    ``(cos, sin)`` pair tables ``[S, 64]``. ``timer(name, fn)`` optionally wraps each kernel launch.
+    ``mod``: this block's rows of :func:`modulation` when the caller computed them for all blocks."""
     run = timer or (lambda name, fn: fn())
     S, dim = h.shape
     heads = dim // HEAD_DIM
     scale = HEAD_DIM**-0.5
-    e = w.scale_shift_table + temb.reshape(6, dim).float()
-    shift, sc, gate, c_shift, c_sc, c_gate = (e[i].contiguous() for i in range(6))
-    one_p_sc, one_p_csc = (1 + sc).contiguous(), (1 + c_sc).contiguous()
+    if mod is None:
+        mod = modulation(w.scale_shift_table[None], temb)[0]
+    shift, one_p_sc, gate, c_shift, one_p_csc, c_gate = (mod[i] for i in range(6))
     cos, sin = rope
 
     a1 = run("adaln", lambda: adaln_quant_2d(h, one_p_sc, shift, eps=eps, norm_type="layer_norm", quant="mx"))
@@ -157,8 +168,14 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
     return run("gemm_down", lambda: mxfp8_linear(inter, w.down, epilogue="gated_residual", residual=h2, gate=c_gate))
 
 
-def dit_forward(blocks, h: torch.Tensor, temb: torch.Tensor, rope, crosses, eps: float = 1e-6, timer=None):
-    """The 40-block loop of one DiT forward (one CFG branch), cross-attention K/V cached."""
-    for w, cross in zip(blocks, crosses):
-        h = block_forward(w, h, temb, rope, cross, eps, timer)
+def dit_forward(blocks, h: torch.Tensor, temb: torch.Tensor, rope, crosses, eps: float = 1e-6, timer=None,
+                tables: torch.Tensor | None = None):
+    """The 40-block loop of one DiT forward (one CFG branch), cross-attention K/V cached. The
+    modulation rows of every block are formed in one batched op up front; ``tables`` optionally
+    holds the blocks' stacked ``scale_shift_table`` ``[B, 6, DIM]`` (built here otherwise)."""
+    if tables is None:
+        tables = torch.stack([w.scale_shift_table for w in blocks])
+    mods = modulation(tables, temb)
+    for i, (w, cross) in enumerate(zip(blocks, crosses)):
+        h = block_forward(w, h, temb, rope, cross, eps, timer, mod=mods[i])
     return h

@@ -6,7 +6,8 @@
 //
 // Statistics use a fixed summation order so the CPU oracle reproduces them bit for bit: every lane
 // sums its own columns sequentially in fp32 (chunk by chunk, column order within a chunk), then the
-// 64 lane sums combine in an xor butterfly (offsets 32, 16, 8, 4, 2, 1). Two passes:
+// 64 lane sums combine in an xor butterfly (offsets 1, 2, 4, 8, 16, 32, done with DPP and lane swaps
+// in the VALU rather than LDS permutes). Two passes:
 //
 //   LayerNorm: mu = S1 / H with S1 = sum x;  var = S2 / H with S2 = sum fl(fl(x - mu)^2)   (fp32)
 //              rstd = fp32(1 / sqrt(fp64(var) + eps))
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
         s1 = s1 + bf16_lo(xp[c][j]);
         s1 = s1 + bf16_hi(xp[c][j]);
       }
-    s1 = wave_sum_f32(s1);
+    s1 = wave_sum_f32_asc(s1);
     mu = s1 / (float)H;
     float s2 = 0.0f;
 #pragma unroll
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
         s2 = s2 + (ok ? q1 : 0.0f);
       }
     }
-    s2 = wave_sum_f32(s2);
+    s2 = wave_sum_f32_asc(s2);
     const float var = s2 / (float)H;
     rs = (float)(1.0 / sqrt((double)var + (double)a.eps));
   } else if (a.norm == WANMI_NORM_RMS) {
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
         s = s + q0;
         s = s + q1;
       }
-    s = wave_sum_f32(s);
+    s = wave_sum_f32_asc(s);
     const float ms = s / (float)H;
     rs = (float)(1.0 / sqrt((double)ms + (double)a.eps));
   }
@@ -216,8 +217,8 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
         int e = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) e = max(e, exp_field(y[j]));
-        e = max(e, __shfl_xor(e, 1, 64));
-        e = max(e, __shfl_xor(e, 2, 64));
+        e = max(e, dpp_i32<0xB1>(e));  // quad_perm(1,0,3,2): lane ^ 1
+        e = max(e, dpp_i32<0x4E>(e));  // quad_perm(2,3,0,1): lane ^ 2
         const int sexp = max(e - 7, 0);
         const float f = mx_inv_scale(sexp);
         u32x2 cv;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
 
   // ---- ROW: codes = e4m3(y / dq), dq = max(amax / 448, 1e-6), fp32 dq appended ----
   if (a.quant == WANMI_QUANT_ROW) {
-    amax = wave_max_f32(amax);
+    amax = wave_max_f32_asc(amax);
     const float dq = fmaxf(amax / 448.0f, 1e-6f);
     // The packed row is H + 4 bytes: codes through a descriptor over H bytes, then the scale.
     const __amdgpu_buffer_rsrc_t r_c =

@@ -39,12 +39,6 @@ struct QKNormArgs {
   float* maxnorm;  // [heads] or null (must be zeroed first)
 };
 
-// v with a DPP lane permutation applied (bound_ctrl: lanes without a source read 0; every control
-// used here has a source for every lane).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
-}
 
 // Up to 40 heads (NCH <= 10) at most 128 VGPRs, four waves per SIMD: the 4095 waves of an S = 32760
 // launch (8 tokens each) are then resident in one round over 256 CUs; at the 130 VGPRs the compiler
@@ -90,7 +84,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
         ss = ss + q0;
         ss = ss + q1;
       }
-    ss = wave_sum_f32(ss);
+    ss = wave_sum_f32_asc(ss);
     const float rs = (float)(1.0 / sqrt((double)(ss / (float)W) + (double)a.eps));
 
     // interleaved: the lane's 4 pairs are the angles 4 (lane & 15) .. +3 of its head; halves: its 8

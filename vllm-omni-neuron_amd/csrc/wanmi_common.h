@@ -178,6 +178,54 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// v with a DPP lane permutation applied (bound_ctrl: lanes without a source read 0; every control
+// used here has a source for every lane).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+// x[l] + x[l ^ 16] and x[l] + x[l ^ 32] in every lane, with v_permlane16_swap / v_permlane32_swap
+// (each exchanges 16- or 32-lane groups of its two operands; with x as both, the pair of results is
+// x[l] and x[l ^ 16] (x[l ^ 32]) in some order, and fp32 addition commutes).
+__device__ __forceinline__ float add_lane_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_lane_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Butterfly sum over the 64 lanes in the order xor 1, 2, 4, 8, 16, 32, entirely in the VALU: quad
+// permutes for 1 and 2; for 4 and 8 the half-row and row mirrors, which equal the xor partners once
+// the quads (8-lane groups) hold one value each, as they do after the steps before; lane swaps for
+// 16 and 32. Every lane ends with the same fp32 value.
+__device__ __forceinline__ float wave_sum_f32_asc(float v) {
+  v = v + dpp_f32<0xB1>(v);   // quad_perm(1,0,3,2): xor 1
+  v = v + dpp_f32<0x4E>(v);   // quad_perm(2,3,0,1): xor 2
+  v = v + dpp_f32<0x141>(v);  // row_half_mirror: xor 4 on uniform quads
+  v = v + dpp_f32<0x140>(v);  // row_mirror: xor 8 on uniform 8-lane groups
+  v = add_lane_xor16(v);
+  return add_lane_xor32(v);
+}
+// The same maximum (order-free).
+__device__ __forceinline__ float wave_max_f32_asc(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
 // Butterfly sum, offsets 32, 16, 8, 4, 2, 1: every lane ends with the same fp32 value (adds commute).
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
