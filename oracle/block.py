@@ -71,11 +71,21 @@ def _attend(q, k, v, scale):
     return _bf16(o.transpose(0, 1).reshape(q.shape[0], -1))
 
 
-def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6):
+def _attend_kernel(q, k, v, scale):
+    """As :func:`_attend`, with the reference attention kernel's rounding points
+    (``const_max_kernel_attention``) instead of exact softmax."""
+    o = oattn.const_max_kernel_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), scale)
+    return _bf16(o.transpose(0, 1).reshape(q.shape[0], -1))
+
+
+def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6, attend=None):
     """MXFP8 block on CPU. ``raw``: bf16/fp32 reference tensors; ``wq``: name -> (codes, scales)
-    numpy in GEMM layout; h [S, dim] bf16; temb [6, dim]; context [S_txt, dim] bf16.
+    numpy in GEMM layout; h [S, dim] bf16; temb [6, dim]; context [S_txt, dim] bf16; ``attend``:
+    the attention of both sub-layers (default exact fp64 softmax, :func:`_attend`; or
+    :func:`_attend_kernel`).
     Returns the intermediates (``a1_codes``/``a1_scales``, ``qkv``, ``attn1``, ``h1``, ``attn2``,
     ``h2``, ``inter``) and ``out``."""
+    attend = attend or _attend
     S, dim = h.shape
     heads = dim // HEAD_DIM
     scale = HEAD_DIM**-0.5
@@ -91,7 +101,7 @@ def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6):
     q = orope.apply_rotary_emb_wan(q, cos[None, :, None], sin[None, :, None])[0]
     k = orope.apply_rotary_emb_wan(k, cos[None, :, None], sin[None, :, None])[0]
     v = qkv[:, 2 * dim :].to(torch.bfloat16).view(S, heads, HEAD_DIM)
-    o1 = _attend(q, k, v, scale)
+    o1 = attend(q, k, v, scale)
     o1c, o1s = _mx_of(o1)
     attn1 = _lin(o1c, o1s, wq["o"], raw["o_b"])
 
@@ -104,7 +114,7 @@ def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6):
     k2 = orope.rms_norm_across_heads(_lin(cc, cs, wq["k2"], raw["k2_b"]).to(torch.bfloat16), raw["norm_k2"], eps)
     v2 = _lin(cc, cs, wq["v2"], raw["v2_b"]).to(torch.bfloat16)
     St = context.shape[0]
-    o2 = _attend(q2, k2.view(St, heads, HEAD_DIM), v2.view(St, heads, HEAD_DIM), scale)
+    o2 = attend(q2, k2.view(St, heads, HEAD_DIM), v2.view(St, heads, HEAD_DIM), scale)
     o2c, o2s = _mx_of(o2)
     attn2 = _lin(o2c, o2s, wq["o2"], raw["o2_b"])
 

@@ -11,9 +11,11 @@ the token rows ``rows`` only, so the checks scale to the 720p sequence:
   stage's input rows (max |err| / max |ref| <= 2e-2, cosine >= 0.999);
 - attention outputs (MX) against MX quantization of fp64 softmax attention over every key, as
   ``test_gpu_block``'s MX stage check does: every element within one e4m3 step plus 2^-7 of its
-  32-block's max, cosine >= 0.999, and at least 98% (self-attention), 90% (cross-attention over 512
-  keys) and 99.5% (FFN GELU) of the codes identical -- the floors the single-block measurements
-  support (99.3%, 92.5% and 99.9% identical).
+  32-block's max, cosine >= 0.999, and at least 98.5% (self-attention), 91% (cross-attention over
+  512 keys) and 99.7% (FFN GELU) of the codes identical -- the floors the measurements support
+  (1560 tokens: 99.3-99.9%, 92.3-92.5%, 99.86-99.87% over four blocks; 720p rows: 99.8%, 92.3%,
+  99.86%), and above what the reference attention kernel's own rounding points keep of the exact
+  result's codes on the same inputs (99.1% self, 90.2% cross).
 """
 
 from __future__ import annotations
@@ -181,7 +183,7 @@ def check_block_rows(pkg, w, h, temb, rope, cross, rows, grid, eps=1e-6, fails=N
     o1 = snap["self_attention"][0]
     att = _attend_rows(q_ref, k, v, scale)
     fails.mx_close(o1.codes[rd], o1.scales[rd], att.to(torch.bfloat16), "self-attention (Q prepared on load, MX)",
-                   min_same=0.98)
+                   min_same=0.985)
     kmax_live = snap["qk_prep"][0]
     kr = float((kmax_live - kn).abs().max() / kn.max())
     print(f"key-norm bound: max rel diff {kr:.2e}")
@@ -212,7 +214,7 @@ def check_block_rows(pkg, w, h, temb, rope, cross, rows, grid, eps=1e-6, fails=N
     v2 = _vt_to_tokens(cross.vt, St)
     o2 = snap["cross_attention"][0]
     att2 = _attend_rows(q2_ref, cross.k, v2, scale)
-    fails.mx_close(o2.codes[rd], o2.scales[rd], att2.to(torch.bfloat16), "cross-attention (MX)", min_same=0.90)
+    fails.mx_close(o2.codes[rd], o2.scales[rd], att2.to(torch.bfloat16), "cross-attention (MX)", min_same=0.91)
 
     # cross o-projection with the plain residual
     h2 = snap["gemm_o2"][0]
@@ -229,7 +231,7 @@ def check_block_rows(pkg, w, h, temb, rope, cross, rows, grid, eps=1e-6, fails=N
     inter = snap["gemm_up"][0]
     lin, _ = _gemm_rows(a3.codes, a3.scales, w.up, rd)
     fails.mx_close(inter.codes[rd], inter.scales[rd], og.gelu_tanh(lin).to(torch.bfloat16), "FFN up + GELU (MX)",
-                   min_same=0.995)
+                   min_same=0.997)
     lin, absg = _gemm_rows(inter.codes, inter.scales, w.down, rd)
     cg = c_gate.double().to(dev)
     ref = h2[rd].double() + lin.to(torch.bfloat16).double() * cg

@@ -11,18 +11,24 @@ Two levels of checking:
    inputs to that stage. adaLN stages (codes, scales, bf16 residual) must be bit-exact; bf16 stage
    outputs (GEMMs, norm/RoPE) must meet max|err|/max|ref| <= 2e-2 and cosine >= 0.999; MX stage
    outputs (attention, GELU) are compared with the oracle's MX quantization of its own bf16 result:
-   at least 98% (self-attention), 90% (cross-attention over 512 keys) and 99.5% (GELU) of the codes
-   identical (measured: 99.3%, 92.5%, 99.9%; the attention's bf16 rounding of its pre-scaled Q and
-   of P moves outputs across e4m3 boundaries, most often over the short text sequence), every
-   element within one e4m3 step plus 2^-7 of its 32-block max, cosine >= 0.999.
+   at least 98.5% (self-attention), 91% (cross-attention over 512 keys) and 99.7% (GELU) of the
+   codes identical, and no fewer than the reference attention kernel's own numerics reach (less
+   0.01), every element within one e4m3 step plus 2^-7 of its 32-block max, cosine >= 0.999.
+   Measured: GPU 99.3%, 92.5%, 99.86%; the reference kernel's rounding points (bf16 P, bf16
+   pre-scaled Q, fp16 shifted scores; ``oracle.attention.const_max_kernel_attention``) on the same
+   stage inputs keep 99.1% (self) and 90.2% (cross) of the exact oracle's codes. Over 512 text keys
+   a bf16 rounding of P or of the pre-scaled Q moves outputs across e4m3 boundaries most often.
 2. end to end: the oracle's MXFP8 block from the same block inputs vs the GPU block output:
-   cosine >= 0.999, relative RMS error <= 3e-2 and max|err|/max|ref| <= 6e-2. These are set by the
-   block's own sensitivity, measured on the oracle alone: moving 0.1% of the input elements by one
-   bf16 ulp moves the oracle's output by max 4.4e-2, RMS 2.3e-2, cosine 0.99973 (the peaked
-   cross-attention over 512 keys amplifies ulp-level differences, and each of the five MX
-   requantization points can then move an element by a full e4m3 step). The stage-wise checks pin
-   every kernel at the single-stage bars. The BF16 eager reference block is reported (the gap is
-   the MXFP8 quantization error), with only a loose cosine asserted.
+   cosine >= 0.999, relative RMS error <= 3e-2 and max|err|/max|ref| <= 6e-2, and relative to
+   the noise floor measured in the same test: the oracle block run with the reference kernel's
+   attention numerics against the exact oracle block (measured max 3.5e-2, RMS 2.4e-2, cosine
+   0.99972; the GPU: 3.2e-2, 2.3e-2, 0.99973). The GPU may be no further from the exact oracle
+   than 1.25x that RMS, 1.5x that max error and 1.5x that cosine deficit. The floor is this large
+   because the block is chaotic at the rounding level: each of its five MX requantization points
+   turns a one-ulp difference into a full e4m3 step for elements near a boundary (moving 0.1% of
+   the input elements by one bf16 ulp moves the oracle's own output by max 4.4e-2, RMS 2.3e-2).
+   The stage-wise checks pin every kernel at the single-stage bars. The BF16 eager reference block
+   is reported (the gap is the MXFP8 quantization error), with only a loose cosine asserted.
 """
 
 import numpy as np
@@ -51,23 +57,42 @@ def _close(got, ref, what, bar=(2e-2, 0.999)):
         FAILS.append((what, rel, cos))
 
 
-def _close_e2e(got, ref, what):
+def _e2e_metrics(got, ref):
     got, ref = got.double().flatten(), ref.double().flatten()
     rel = float((got - ref).abs().max() / ref.abs().max())
     rms = float((got - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt())
     cos = float(torch.nn.functional.cosine_similarity(got, ref, dim=0))
+    return rel, rms, cos
+
+
+def _close_e2e(got, ref, what, noise=None):
+    """Absolute bars, and with ``noise`` (the metrics of the reference kernel's numerics against the
+    same exact oracle) bars relative to it: the GPU may sit no further from the exact oracle than
+    the reference's own attention numerics do, with a margin (1.25x RMS, 1.5x max error, 1.5x the
+    cosine deficit)."""
+    rel, rms, cos = _e2e_metrics(got, ref)
     print(f"{what}: max rel_err {rel:.2e} rms rel_err {rms:.2e} cos {cos:.6f}")
     assert cos >= 0.999 and rms <= 3e-2 and rel <= 6e-2, (what, rel, rms, cos)
+    if noise is not None:
+        n_rel, n_rms, n_cos = noise
+        assert rms <= 1.25 * n_rms and rel <= 1.5 * n_rel and 1 - cos <= 1.5 * (1 - n_cos), (what, (rel, rms, cos), noise)
 
 
-def _mx_close(got_mx, ref_bf16, what, min_same):
+def _mx_close(got_mx, ref_bf16, what, min_same, kernel_bf16=None):
     """GPU MX output vs MX(oracle bf16 output): codes mostly identical; every element within one
-    e4m3 step of itself plus 2^-7 of its 32-block's max (bf16-level absolute error of the stage)."""
+    e4m3 step of itself plus 2^-7 of its 32-block's max (bf16-level absolute error of the stage).
+    ``kernel_bf16``: the same stage through the reference attention kernel's rounding points; the
+    share of its MX codes identical to the exact oracle's is printed beside the GPU's."""
     rc, rs = omx.mx_quantize(ref_bf16.float().numpy())
     gc, gs = _mx_np(got_mx)
     g = omx.mx_dequantize(gc, gs)
     r = omx.mx_dequantize(rc, rs)
     same = float((gc == rc).mean())
+    if kernel_bf16 is not None:
+        kc, _ = omx.mx_quantize(kernel_bf16.float().numpy())
+        same_k = float((kc == rc).mean())
+        print(f"{what}: reference kernel numerics vs exact: identical codes {same_k:.4f}")
+        min_same = max(min_same, same_k - 0.01)
     bmax = np.repeat(np.abs(r).reshape(*r.shape[:-1], -1, 32).max(axis=-1), 32, axis=-1)
     tol = 2.0**-3 * np.maximum(np.abs(g), np.abs(r)) + 2.0**-7 * bmax + 1e-30
     worst = float((np.abs(g - r) / tol).max())
@@ -161,8 +186,9 @@ def test_block_stagewise(pkg, dev, run):
     k = qkv_post[:, dim : 2 * dim].view(S, heads, D)
     v = v_tok[:S]
     o1 = snap["self_attention"][0]
-    _mx_close(o1, oblock._attend(refn["norm_q"].to(torch.bfloat16).view(S, heads, D), k, v, s),
-              "self-attention with Q RMSNorm+RoPE on load (MX out)", 0.98)
+    qn = refn["norm_q"].to(torch.bfloat16).view(S, heads, D)
+    _mx_close(o1, oblock._attend(qn, k, v, s), "self-attention with Q RMSNorm+RoPE on load (MX out)", 0.985,
+              kernel_bf16=oblock._attend_kernel(qn, k, v, s))
     # o-proj with the gated residual in its epilogue, from the GPU's MX attention output:
     # h1 = bf16(h + bf16(o1 @ Wo + b) * gate)
     h1 = snap["gemm_o"][0].cpu()
@@ -199,7 +225,8 @@ def test_block_stagewise(pkg, dev, run):
     _close(v_gpu.reshape(512, dim), v2, "cross V (projected once)")
     # cross-attention from the GPU's q2 and cached K/V
     o2 = snap["cross_attention"][0]
-    _mx_close(o2, oblock._attend(q2.view(S, heads, D), r["cross"].k.cpu(), v_gpu, s), "cross-attention (MX out)", 0.90)
+    _mx_close(o2, oblock._attend(q2.view(S, heads, D), r["cross"].k.cpu(), v_gpu, s), "cross-attention (MX out)", 0.91,
+              kernel_bf16=oblock._attend_kernel(q2.view(S, heads, D), r["cross"].k.cpu(), v_gpu, s))
     # cross o-proj with the residual in its epilogue: h2 = bf16(h1 + bf16(o2 @ Wo2 + b))
     h2 = snap["gemm_o2"][0].cpu()
     attn2_ref = oblock._lin(*_mx_np(o2), wq["o2"], raw["o2_b"])
@@ -217,7 +244,7 @@ def test_block_stagewise(pkg, dev, run):
     # FFN up + GELU + MX from the GPU's a3
     inter = snap["gemm_up"][0]
     up = oblock._deq(*_mx_np(a3)) @ oblock._deq(*wq["up"]).T + raw["up_b"].float()
-    _mx_close(inter, torch.nn.functional.gelu(up, approximate="tanh").to(torch.bfloat16), "FFN up + GELU (MX out)", 0.995)
+    _mx_close(inter, torch.nn.functional.gelu(up, approximate="tanh").to(torch.bfloat16), "FFN up + GELU (MX out)", 0.997)
     # down projection + gated residual from the GPU's MX intermediate
     ffn = oblock._lin(*_mx_np(inter), wq["down"], raw["down_b"])
     ref_out = (h2.float().cpu() + ffn * c_gate).to(torch.bfloat16).float()
@@ -229,8 +256,14 @@ def test_block_stagewise(pkg, dev, run):
 def test_block_end_to_end(run):
     r = run
     ref = oblock.mxfp8_block(r["raw"], r["wq"], r["h"], r["temb"], r["ctx"], GRID)
-    _close_e2e(r["out"], ref["out"], "block output vs MXFP8 oracle block")
-    _close_e2e(r["out"] - r["h"].float(), ref["out"] - r["h"].float(), "block update (out - h) vs oracle")
+    refk = oblock.mxfp8_block(r["raw"], r["wq"], r["h"], r["temb"], r["ctx"], GRID, attend=oblock._attend_kernel)
+    hf = r["h"].float()
+    n_out, n_upd = _e2e_metrics(refk["out"], ref["out"]), _e2e_metrics(refk["out"] - hf, ref["out"] - hf)
+    print("reference kernel numerics vs exact oracle block: output max rel {:.2e} rms {:.2e} cos {:.6f}".format(*n_out))
+    print("reference kernel numerics vs exact oracle block: update max rel {:.2e} rms {:.2e} cos {:.6f}".format(*n_upd))
+    _close_e2e(r["out"], ref["out"], "block output vs MXFP8 oracle block", noise=n_out)
+    _close_e2e(r["out"] - hf, ref["out"] - hf, "block update (out - h) vs oracle", noise=n_upd)
+    _close_e2e(r["out"], refk["out"], "block output vs oracle block with the kernel's attention numerics")
     eager = oblock.bf16_eager_block(r["raw"], r["h"], r["temb"], r["ctx"], GRID).float()
     cos_e = float(torch.nn.functional.cosine_similarity(r["out"].double().flatten(), eager.double().flatten(), dim=0))
     d_e = float(torch.nn.functional.cosine_similarity((r["out"] - r["h"].float()).double().flatten(),

@@ -3,6 +3,11 @@
 - exact attention vs a brute-force loop on tiny shapes;
 - constant-max attention equals exact softmax attention and is invariant to the subtracted
   constant; a fully underflowed row hits the 1e-37 sum floor and returns zeros;
+- the reference kernel's rounding points (``const_max_kernel_attention``): identical keys give the
+  exact mean of V whatever the rounding; a two-key case whose bf16 P is known by hand
+  (exp(-1.09765625) = 0.33365... rounds to 0.333984375) checks that both the numerator and the
+  row sum use the rounded P; on random data the result stays within bf16-level error of exact
+  attention;
 - Wan RoPE: angles match the closed form theta^(-2i/dim) * position per axis, the rotation preserves
   norms, and interleaved RoPE equals rotate-half RoPE on de-interleaved channels (the equivalence
   the reference's fused QKV path relies on, row_mx_loaders.py:26-39, row_mx_modules.py:51-76).
@@ -50,6 +55,38 @@ def test_const_max_underflow_clamp():
     v = torch.randn(1, 6, 128)
     out = oa.const_max_attention(q, k, v, 1.0, c=torch.full((1, 4, 1), 1e4, dtype=torch.float64))
     assert bool((out == 0).all())
+
+
+def test_kernel_numerics_identical_keys_give_the_mean():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(5, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 128, generator=g).to(torch.bfloat16).expand(7, 128)
+    v = torch.randn(7, 128, generator=g).to(torch.bfloat16)
+    out = oa.const_max_kernel_attention(q, k, v, 128**-0.5)
+    assert torch.allclose(out, v.double().mean(dim=0).expand(5, 128), atol=1e-12)
+
+
+def test_kernel_numerics_round_p_in_both_sums():
+    # q = (1, 0), keys (2, 0) and (0.90234375, 1), scale 1: c = 1 * 1 * max(2, 1.347) = 2, scores 2
+    # and 0.90234375, shifted 0 and -1.09765625 (exact in fp16), P = 1 and bf16(0.3336521...) =
+    # 0.333984375. With V = I the output is (1, p) / (1 + p) for that rounded p.
+    q = torch.tensor([[1.0, 0.0]]).to(torch.bfloat16)
+    k = torch.tensor([[2.0, 0.0], [0.90234375, 1.0]]).to(torch.bfloat16)
+    v = torch.eye(2).to(torch.bfloat16)
+    out = oa.const_max_kernel_attention(q, k, v, 1.0)
+    p = 0.333984375
+    assert math.exp(-1.09765625) != p
+    assert torch.allclose(out, torch.tensor([[1.0 / (1 + p), p / (1 + p)]], dtype=torch.float64), atol=1e-12)
+
+
+def test_kernel_numerics_close_to_exact_attention():
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(2, 48, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+    s = 128**-0.5
+    ref = oa.torch_attend(q, k, v, s, dtype=torch.float64)
+    out = oa.const_max_kernel_attention(q, k, v, s)
+    err = (out - ref).abs().max()
+    assert 0 < err <= 2.0**-7 * v.double().abs().max()
 
 
 def test_wan_rope_closed_form():
