@@ -59,7 +59,8 @@ def layer_norm_stats(x: np.ndarray, eps: float):
     lm = _lane_major(x)
     mu = (_ordered_sum(lm) / np.float32(H)).astype(np.float32)
     d = (lm - mu[:, :, None]).astype(np.float32)
-    q = (d * d).astype(np.float32)
+    with np.errstate(over="ignore"):  # fp32 squares of extreme rows overflow to inf, as on the GPU
+        q = (d * d).astype(np.float32)
     q = np.where(_valid_lane_major(T, H)[None], q, np.float32(0.0))
     var = (_ordered_sum(q) / np.float32(H)).astype(np.float32)
     rstd = (1.0 / np.sqrt(var.astype(np.float64) + np.float64(np.float32(eps)))).astype(np.float32)
