@@ -63,18 +63,30 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 // Each tensor is addressed through a buffer descriptor based at the current row (scalar registers),
 // one per-lane byte offset and the chunk offset in the scalar soffset field, so no per-chunk vector
 // address is ever materialized; descriptor extents mask the columns past H in a partial chunk.
-template <int NCH>
+//
+// kLdsMod (no residual, both modulation vectors given, H <= 5120): the workgroup's four waves copy
+// the fp32 mul and add vectors into LDS once (direct-to-LDS loads) and read them from there. Read
+// per row from L2 instead, the two vectors are 8 bytes per column against the row's 2 (x) + 1
+// (codes) -- four times the row's own traffic through the texture unit, the pass's busiest unit.
+// The LDS copy holds, per vector, chunk c's first four floats of every lane (lane-major, 16 bytes
+// each), then the second four, so that a lane's 16-byte reads of one chunk are consecutive across
+// lanes (bank-conflict free).
+template <int NCH, bool kLdsMod = false>
 __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float smod[kLdsMod ? 2 * 2 * NCH * 64 * 4 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.H;
   const int nch = a.nch;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= a.T) return;
-  const int64_t rbase = row * (int64_t)H;
+  const bool live = row < a.T;
+  // every wave of the workgroup takes part in the vectors' copy (and its barrier); rows past T
+  // load nothing (empty descriptor) and leave after it
+  if (!kLdsMod && !live) return;
+  const int64_t rbase = live ? row * (int64_t)H : 0;
 
-  const __amdgpu_buffer_rsrc_t r_x = rsrc(a.hidden + rbase, 2 * (int64_t)H);
+  const __amdgpu_buffer_rsrc_t r_x = rsrc(a.hidden + rbase, live ? 2 * (int64_t)H : 0);
   uint32_t xp[NCH][4];  // the row's x as packed bf16 pairs (exact; also the residual sum)
 
   // ---- load (and optional gated residual add, x = bf16(h * gate + res)) ----
@@ -120,6 +132,18 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
     }
   }
   // Columns past H were read as zero through the descriptor extent.
+  if constexpr (kLdsMod) {
+    constexpr int kPerVec = 2 * NCH;  // 1 KiB loads per vector: halves x chunks
+    const uint32_t base = lds_addr(smod);
+    const u32x4 rm = buffer_rsrc(a.mul, 4u * (uint32_t)H), ra = buffer_rsrc(a.add, 4u * (uint32_t)H);
+    for (int k = wave; k < 2 * kPerVec; k += 4) {
+      const int kk = k % kPerVec, hh = kk / NCH, c = kk % NCH;
+      lds_dma_b128(k < kPerVec ? rm : ra, (uint32_t)(c * 512 + 8 * lane + 4 * hh) * 4, base + (uint32_t)k * 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    if (!live) return;
+  }
 
   // ---- statistics (fixed-order fp32 sums, see the file header) ----
   float mu = 0.0f, rs = 1.0f;
@@ -192,8 +216,16 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
       {
         float mv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
         float av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (a.mul) load8f(r_m, lane, c, mv);
-        if (a.add) load8f(r_a, lane, c, av);
+        if constexpr (kLdsMod) {
+          const float4* sm = reinterpret_cast<const float4*>(smod);
+          const float4 m0 = sm[c * 64 + lane], m1 = sm[(NCH + c) * 64 + lane];
+          const float4 a0 = sm[(2 * NCH + c) * 64 + lane], a1 = sm[(3 * NCH + c) * 64 + lane];
+          mv[0] = m0.x, mv[1] = m0.y, mv[2] = m0.z, mv[3] = m0.w, mv[4] = m1.x, mv[5] = m1.y, mv[6] = m1.z, mv[7] = m1.w;
+          av[0] = a0.x, av[1] = a0.y, av[2] = a0.z, av[3] = a0.w, av[4] = a1.x, av[5] = a1.y, av[6] = a1.z, av[7] = a1.w;
+        } else {
+          if (a.mul) load8f(r_m, lane, c, mv);
+          if (a.add) load8f(r_a, lane, c, av);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           float v = (j & 1) ? bf16_hi(xp[c][j >> 1]) : bf16_lo(xp[c][j >> 1]);
@@ -264,7 +296,13 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
 template <int NCH>
 static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.T + 3) / 4;
-  hipLaunchKernelGGL(adaln_quant_kernel<NCH>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  if constexpr (NCH <= 10) {
+    if (!a.residual && a.mul && a.add) {
+      hipLaunchKernelGGL((adaln_quant_kernel<NCH, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((adaln_quant_kernel<NCH, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
 }  // namespace wanmi
