@@ -46,14 +46,29 @@ struct QKNormArgs {
 // second round (190 vs 159 us). Wider rows keep the registers they need.
 // kHalves: rotate-half pairs (i, i+64) (the drop-in path for the reference's de-interleaved
 // weights; it keeps the register budget but may spill a little), else interleaved pairs.
+// Up to 40 heads the fp32 gamma (8 bytes per column, as much as the token's own bf16 read and write)
+// is copied into LDS once per workgroup of 32 tokens instead of being read from L2 per token: per
+// chunk, every lane's first four values (16 bytes, lane-major), then the second four.
 template <int NCH, bool kHalves>
 __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
 #pragma clang fp contract(off)
+  constexpr bool kLdsGamma = NCH <= 10;
+  __shared__ __attribute__((aligned(16))) float sgam[kLdsGamma ? 2 * NCH * 64 * 4 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = a.heads * 128;
   const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * a.tokens_per_wave;
   const __amdgpu_buffer_rsrc_t r_g = make_rsrc(a.gamma, 4 * (int64_t)W);
+  if constexpr (kLdsGamma) {
+    const u32x4 rg = buffer_rsrc(a.gamma, 4u * (uint32_t)W);  // columns past W read as zero
+    const uint32_t base = lds_addr(sgam);
+    for (int k = wave; k < 2 * NCH; k += 4) {
+      const int hh = k / NCH, c = k % NCH;
+      lds_dma_b128(rg, (uint32_t)(c * 512 + 8 * lane + 4 * hh) * 4, base + (uint32_t)k * 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+  }
   float kmx[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) kmx[c] = 0.0f;
@@ -111,8 +126,14 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (c < a.nch) {
-        const u32x4 g0 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32, c * 2048, 0);
-        const u32x4 g1 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32 + 16, c * 2048, 0);
+        u32x4 g0, g1;
+        if constexpr (kLdsGamma) {
+          g0 = reinterpret_cast<const u32x4*>(sgam)[c * 64 + lane];
+          g1 = reinterpret_cast<const u32x4*>(sgam)[(NCH + c) * 64 + lane];
+        } else {
+          g0 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32, c * 2048, 0);
+          g1 = __builtin_amdgcn_raw_buffer_load_b128(r_g, lane * 32 + 16, c * 2048, 0);
+        }
         const float gv[8] = {__uint_as_float(g0[0]), __uint_as_float(g0[1]), __uint_as_float(g0[2]),
                              __uint_as_float(g0[3]), __uint_as_float(g1[0]), __uint_as_float(g1[1]),
                              __uint_as_float(g1[2]), __uint_as_float(g1[3])};
