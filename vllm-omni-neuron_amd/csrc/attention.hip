@@ -165,6 +165,7 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) uint8_t sK[kStages][kTileK];
   __shared__ __attribute__((aligned(16))) uint8_t sV[kStages][kTileV];
+  __shared__ __attribute__((aligned(16))) float sgam[kWaves][256];  // each wave's copy of the head's gamma
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -229,7 +230,10 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   // (about 9 us per workgroup, 40% of a cross-attention launch).
   const bool qprep = a.q_sumsq != nullptr;
   const bool qrope = qprep && a.q_cos != nullptr;
-  const __amdgpu_buffer_rsrc_t r_gm = attn_rsrc(qprep ? a.q_gamma + h * 128 : nullptr, qprep ? 128 * 4 : 0);
+  // The head's gamma (128 floats, the same for every query) goes to LDS, one copy per wave so that no
+  // barrier is needed before the wave reads it; read per lane from L2 it was 16 loads of 1 KiB per
+  // wave through the texture unit, more than the wave's Q itself.
+  if (qprep) lds_dma_b128(buffer_rsrc(a.q_gamma + h * 128, 128 * 4), (uint32_t)lane * 16, lds_addr(sgam[wave]));
   const __amdgpu_buffer_rsrc_t r_cs =
       attn_rsrc(qrope ? a.q_cos + (qvalid > 0 ? q0 * 64 : 0) : nullptr, qrope && qvalid > 0 ? qvalid * 64 * 4 : 0);
   const __amdgpu_buffer_rsrc_t r_sn =
@@ -239,29 +243,45 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   for (int t = 0; t < 8; ++t)
     qv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
   if (qprep) {
-    // descriptors of absent inputs have an empty extent, so their loads read zeros and stay unused
-    u32x4 g0[8], g1[8], cv[8], sv[8];
+    // the RoPE tables only when there is a rotation (the cross-attention query has none)
+    u32x4 cv[8], sv[8];
+    if (qrope) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      g0[t] = __builtin_amdgcn_raw_buffer_load_b128(r_gm, (uint32_t)((16 * t + 8 * hq) * 4), 0, 0);
-      g1[t] = __builtin_amdgcn_raw_buffer_load_b128(r_gm, (uint32_t)((16 * t + 8 * hq + 4) * 4), 0, 0);
-      cv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_cs, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
-      sv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_sn, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
+      for (int t = 0; t < 8; ++t) {
+        cv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_cs, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
+        sv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_sn, (uint32_t)((col * 64 + 8 * t + 4 * hq) * 4), 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) cv[t] = sv[t] = u32x4{0u, 0u, 0u, 0u};
     }
     const __amdgpu_buffer_rsrc_t r_ss = attn_rsrc(a.q_sumsq + (qvalid > 0 ? q0 * a.qss_ld : 0),
                                                   qvalid > 0 ? ((qvalid - 1) * a.qss_ld + a.heads) * 4 : 0);
     float ss = 0.0f;
     if (a.heads <= 40) {
-      // ten unconditional loads; blocks past `heads` (another row's partials, or zeros past the
-      // extent) are masked to zero and add exactly nothing, so the sum is the block-ordered one
-      u32x4 pv[10];
+      // Five unconditional loads per lane: the lanes of half hq read blocks 20 hq .. 20 hq + 19 of
+      // their query's partials, and a lane swap with lane ^ 32 (which holds the same query's other
+      // twenty) gives every lane all forty: v_permlane32_swap of x with itself returns the lower
+      // half's value first and the upper half's second in every lane. Blocks past `heads` (another
+      // row's partials, or zeros past the extent) are masked to zero and add exactly nothing, so
+      // the sum is the block-ordered one.
+      u32x4 pv[5];
 #pragma unroll
-      for (int i = 0; i < 10; ++i)
-        pv[i] = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + 4 * i) * 4), 0, 0);
+      for (int i = 0; i < 5; ++i)
+        pv[i] = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + 20 * hq + 4 * i) * 4), 0, 0);
+      float lo[20], hi[20];
 #pragma unroll
-      for (int i = 0; i < 10; ++i)
+      for (int i = 0; i < 5; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ss = ss + (4 * i + j < a.heads ? __uint_as_float(pv[i][j]) : 0.0f);
+        for (int j = 0; j < 4; ++j) {
+          const auto r = __builtin_amdgcn_permlane32_swap(pv[i][j], pv[i][j], false, false);
+          lo[4 * i + j] = __uint_as_float(r[0]);
+          hi[4 * i + j] = __uint_as_float(r[1]);
+        }
+#pragma unroll
+      for (int b = 0; b < 20; ++b) ss = ss + (b < a.heads ? lo[b] : 0.0f);
+#pragma unroll
+      for (int b = 0; b < 20; ++b) ss = ss + (20 + b < a.heads ? hi[b] : 0.0f);
     } else {
       for (int b4 = 0; b4 < a.heads; b4 += 4) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + b4) * 4), 0, 0);
@@ -270,13 +290,15 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
       }
     }
     const float rr = (float)(1.0 / sqrt((double)(ss / (float)(a.heads * 128)) + (double)a.q_eps));
+    // every load of the prologue is in (the math below needs them all), the gamma copy included
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const float4* gl = reinterpret_cast<const float4*>(sgam[wave]);
     // x_hat = bf16((x rrms) gamma), then the pair rotation (a cos - b sin, a sin + b cos) -> bf16:
     // the same operations, in the same order, as the separate Q/K preparation pass
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const float gv[8] = {__uint_as_float(g0[t][0]), __uint_as_float(g0[t][1]), __uint_as_float(g0[t][2]),
-                           __uint_as_float(g0[t][3]), __uint_as_float(g1[t][0]), __uint_as_float(g1[t][1]),
-                           __uint_as_float(g1[t][2]), __uint_as_float(g1[t][3])};
+      const float4 ga = gl[4 * t + 2 * hq], gb = gl[4 * t + 2 * hq + 1];
+      const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float a0 = round_bf16((bf16_lo(qv[t][j]) * rr) * gv[2 * j]);
