@@ -11,7 +11,7 @@
 // a single "ring step", c_i is kept in fp32 (the reference rounds it to bf16; the result does not
 // depend on c), and exp runs as exp2 with log2(e) folded into the scale.
 //
-// Mapping: a workgroup owns 128 queries of one head (4 waves x 32) and walks the keys in tiles of
+// Mapping: a workgroup owns 256 queries of one head (8 waves x 32) and walks the keys in tiles of
 // 64. Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K from LDS as the A operand,
 // its 32 queries' Q fragments resident in registers as the B operand), so every lane ends up owning
 // one query column: the row sum of P is lane-local and P^T is already laid out as the B operand of
@@ -29,6 +29,10 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int BKV = 64;            // keys per LDS tile (two 32-key halves)
 constexpr int kStages = 4;         // LDS ring depth in tiles
 constexpr float kSumFloor = 1e-37f;
+#ifndef WANMI_CROSS_HEADS_PER_GROUP
+#define WANMI_CROSS_HEADS_PER_GROUP 5
+#endif
+constexpr int kCrossHeadsPerGroup = WANMI_CROSS_HEADS_PER_GROUP;  // heads per workgroup, short key sequences
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kAttnRsrcWord3);
@@ -60,6 +64,7 @@ struct AttnArgs {
   const float* q_cos;
   const float* q_sin;
   float q_eps;
+  int heads_per_group;  // attention_head_group_kernel: consecutive heads per workgroup (divides heads)
 };
 
 // LDS tiles, a ring of kStages (tile t in slot t % kStages):
@@ -449,6 +454,278 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   }
 }
 
+// Several heads per workgroup, for short key sequences (cross-attention over the text tokens): with
+// 8 key tiles per head, a workgroup that owned one head spent about as long in its prologue (Q, its
+// norm inputs and the first K/V tiles, all waited on before the first MFMA) as in its key loop.
+// Here one workgroup walks `heads_per_group` consecutive heads of its 256 queries. The tiles of its
+// heads form one sequence g = hl * ntiles + kt through the same LDS ring, so the next head's first
+// K/V tiles load while the current head finishes; the next head's Q (and gamma) load during the
+// current head's drain and output; the queries' across-heads 1/rms, the same for every head, is
+// computed once. Per head, the math is that of attention_const_max_kernel<true, false> (the bf16
+// row sum of the short-key instantiation) in the same order, so the results are bit-identical.
+// Requires ntiles >= 3, no RoPE on Q, K of one head within one descriptor (the host checks).
+__global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) uint8_t sK[kStages][kTileK];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[kStages][kTileV];
+  __shared__ __attribute__((aligned(16))) float sgam[kWaves][256];  // each wave's copy of the head's gamma
+  __shared__ __attribute__((aligned(16))) uint8_t sStg[4][4096];    // MX output staging of waves 4-7
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hpw = a.heads_per_group;
+  const int h_first = blockIdx.y * hpw;
+  const int64_t q0 = (int64_t)blockIdx.x * BQ + wave * 32;
+  const int col = lane & 31;
+  const int hq = lane >> 5;
+  const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
+
+  const int k_row = lane >> 4, k_pc = lane & 15;
+  const int v_row = lane >> 3, v_pc = lane & 7;
+  // Tile kt of the group's head hl into slot (hl * ntiles + kt) % kStages; same lane mapping and
+  // descriptors as attention_const_max_kernel, built per tile from the head.
+  auto issue_tile = [&](int hl, int kt) {
+    const int b = (hl * ntiles + kt) % kStages;
+    const int hd = h_first + hl;
+    const u32x4 r_k = buffer_rsrc(a.k + hd * a.k_hs, (uint32_t)(((a.Sk - 1) * a.k_ss + 128) * 2));
+    const u32x4 r_v = buffer_rsrc(a.vt + (int64_t)hd * 128 * a.vt_ld, (uint32_t)(128 * a.vt_ld * 2));
+    const int64_t kbase = (int64_t)kt * BKV;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = wave * 8 + i * 4 + k_row;
+      const int c = k_pc ^ (key & 15);
+      lds_dma_b128_hot(r_k, (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int d = wave * 16 + i * 8 + v_row;
+      const int c = v_pc ^ (d & 7) ^ ((d >> 3) & 1);
+      lds_dma_b128_hot(r_v, (uint32_t)((d * a.vt_ld + c * 8) * 2), (uint32_t)(kbase * 2),
+                       lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
+    }
+  };
+  // tile g + 2 of tile g = (hl, kt), if the group has one (ntiles >= 3: at most one wrap)
+  auto issue_ahead = [&](int hl, int kt) {
+    int kt2 = kt + 2, hl2 = hl;
+    if (kt2 >= ntiles) {
+      kt2 -= ntiles;
+      ++hl2;
+    }
+    if (hl2 < hpw) issue_tile(hl2, kt2);
+  };
+  issue_tile(0, 0);
+  issue_tile(0, 1);
+  issue_tile(0, 2);
+
+  const int64_t qvalid = a.Sq - q0 < 32 ? (a.Sq - q0 > 0 ? a.Sq - q0 : 0) : 32;
+  auto issue_q = [&](int hd, u32x4 (&qv)[8]) {
+    const __amdgpu_buffer_rsrc_t r_q = attn_rsrc(a.q + hd * a.q_hs + (qvalid > 0 ? q0 * a.q_ss : 0),
+                                                 qvalid > 0 ? ((qvalid - 1) * a.q_ss + 128) * 2 : 0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      qv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+  };
+  const bool qprep = a.q_sumsq != nullptr;
+  auto issue_gamma = [&](int hd) {
+    if (qprep) lds_dma_b128(buffer_rsrc(a.q_gamma + hd * 128, 128 * 4), (uint32_t)lane * 16, lds_addr(sgam[wave]));
+  };
+  issue_gamma(h_first);
+  u32x4 qv[8];
+  issue_q(h_first, qv);
+  // the queries' across-heads 1/rms, from the partial sums in block order (as in
+  // attention_const_max_kernel: lane halves read twenty blocks each and swap)
+  float rr = 0.0f;
+  if (qprep) {
+    const __amdgpu_buffer_rsrc_t r_ss = attn_rsrc(a.q_sumsq + (qvalid > 0 ? q0 * a.qss_ld : 0),
+                                                  qvalid > 0 ? ((qvalid - 1) * a.qss_ld + a.heads) * 4 : 0);
+    float ss = 0.0f;
+    if (a.heads <= 40) {
+      u32x4 pv[5];
+#pragma unroll
+      for (int i = 0; i < 5; ++i)
+        pv[i] = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + 20 * hq + 4 * i) * 4), 0, 0);
+      float lo[20], hi[20];
+#pragma unroll
+      for (int i = 0; i < 5; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto r = __builtin_amdgcn_permlane32_swap(pv[i][j], pv[i][j], false, false);
+          lo[4 * i + j] = __uint_as_float(r[0]);
+          hi[4 * i + j] = __uint_as_float(r[1]);
+        }
+#pragma unroll
+      for (int b = 0; b < 20; ++b) ss = ss + (b < a.heads ? lo[b] : 0.0f);
+#pragma unroll
+      for (int b = 0; b < 20; ++b) ss = ss + (20 + b < a.heads ? hi[b] : 0.0f);
+    } else {
+      for (int b4 = 0; b4 < a.heads; b4 += 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r_ss, (uint32_t)((col * a.qss_ld + b4) * 4), 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = ss + __uint_as_float(v[j]);
+      }
+    }
+    rr = (float)(1.0 / sqrt((double)(ss / (float)(a.heads * 128)) + (double)a.q_eps));
+  }
+  const int sk_rem = (int)(a.Sk - (int64_t)(ntiles - 1) * BKV);
+
+  for (int hl = 0; hl < hpw; ++hl) {
+    const int h = h_first + hl;
+    const int g0 = hl * ntiles;
+    // Loop-invariant per-lane values passed through an empty asm per head: otherwise the compiler
+    // hoists every lane's 64-bit output offsets out of the head loop and spills them.
+    int64_t o_ss = a.o_ss, o_ds = a.o_ds, os_ss = a.os_ss;
+    asm volatile("" : "+s"(o_ss), "+s"(o_ds), "+s"(os_ss));
+    // This head's Q and gamma are in once every outstanding load is (tiles g0 and g0 + 1 were
+    // issued before them).
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    if (qprep) {
+      const float4* gl = reinterpret_cast<const float4*>(sgam[wave]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float4 ga = gl[4 * t + 2 * hq], gb = gl[4 * t + 2 * hq + 1];
+        const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = round_bf16((bf16_lo(qv[t][j]) * rr) * gv[2 * j]);
+          const float b0 = round_bf16((bf16_hi(qv[t][j]) * rr) * gv[2 * j + 1]);
+          qv[t][j] = pack_bf16x2(a0, b0);
+        }
+      }
+    }
+    bf16x8 qf[8];
+    float qn2 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_lo(qv[t][j]), hi = bf16_hi(qv[t][j]);
+        qn2 = qn2 + lo * lo;
+        qn2 = qn2 + hi * hi;
+      }
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(bf16_lo(qv[t][j]) * a.scale_log2, bf16_hi(qv[t][j]) * a.scale_log2);
+      qf[t] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    qn2 = qn2 + __shfl_xor(qn2, 32, 64);
+    const float c2 = a.scale_log2 * sqrtf(qn2) * a.kmax[h];
+    f32x16 negc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negc[r] = -c2;
+    f32x16 acc_o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.0f;
+    float lsum = 0.0f;
+
+    // The head's first barrier: after it, the slot of tile g0 + 2 (tile g0 - 2's) is free.
+    __syncthreads();
+    if (hl > 0) issue_tile(hl, 2);
+    const int s0 = g0 % kStages;
+    f32x16 s_prev = qk_half(sK[s0], 0, qf, negc, col, hq);
+    pipeline_step<false, true>(sK[s0], 1, sV[s0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    // steady tiles: outstanding are tiles g and g + 1 (four loads per wave each)
+    for (int t = 1; t < ntiles - 1; ++t) {
+      const int slot = (g0 + t) % kStages;
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
+      __syncthreads();
+      issue_ahead(hl, t);
+      const int prev = (slot + kStages - 1) % kStages;
+      pipeline_step<false, true>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+      pipeline_step<false, true>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    }
+    // the last tile: the next head's tile 0 is outstanding behind it, unless this head is the last
+    const int g_last = g0 + ntiles - 1;
+    if (hl + 1 < hpw)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    issue_ahead(hl, ntiles - 1);
+    {
+      const uint8_t* kc = sK[g_last % kStages];
+      pipeline_step<false, true>(kc, 0, sV[(g_last - 1) % kStages], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+      pipeline_step<true, true>(kc, 1, sV[g_last % kStages], 0, qf, negc, s_prev, acc_o, lsum, col, hq, sk_rem);
+    }
+    // the next head's Q and gamma load while this head drains and writes its output
+    if (hl + 1 < hpw) {
+      issue_q(h + 1, qv);
+      issue_gamma(h + 1);
+    }
+    {
+      bf16x8 pf[2];
+      softmax_half<true, true>(s_prev, hq, sk_rem - 32, lsum, pf);
+      pv_half(sV[g_last % kStages], 1, pf, acc_o, col, hq);
+    }
+
+    lsum = lsum + __shfl_xor(lsum, 32, 64);
+    const float inv = 1.0f / fmaxf(lsum, kSumFloor);
+    const int64_t qi = q0 + col;
+    const bool qok = qi < a.Sq;
+    if (a.out_mode == WANMI_ATTN_OUT_TOKEN) {
+      uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi * o_ss;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = dt * 32 + gi * 8 + hq * 4;
+          const float v0 = acc_o[dt][gi * 4] * inv, v1 = acc_o[dt][gi * 4 + 1] * inv;
+          const float v2 = acc_o[dt][gi * 4 + 2] * inv, v3 = acc_o[dt][gi * 4 + 3] * inv;
+          if (qok) *reinterpret_cast<uint2*>(out + d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+        }
+    } else if (a.out_mode == WANMI_ATTN_OUT_DMAJOR) {
+      uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = dt * 32 + (r >> 2) * 8 + hq * 4 + (r & 3);
+          if (qok) out[d * o_ds] = (uint16_t)(pack_bf16x2(acc_o[dt][r] * inv, 0.0f) & 0xFFFFu);
+        }
+    } else {
+      // MX rows staged as in attention_const_max_kernel. The staging area must be one that no wave
+      // reads after the last tile's barrier and that no load in flight writes: waves 0-3 use the K
+      // half of tile g_last - 1's slot (that K was read within tile g_last - 1; the slot's V is
+      // still read in tile g_last's first step, and the next head's tiles g_last + 1 and + 2 are in
+      // the two other slots; tile g_last + 3 goes into this slot only after the next head's first
+      // barrier, which every wave reaches after reading its staging back), waves 4-7 use sStg.
+      uint8_t* stg = wave < 4 ? sK[(g_last + kStages - 1) % kStages] + wave * 4096 : sStg[wave & 3];
+      uint32_t sw = 0;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        float y[16];
+        int e = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          y[r] = round_bf16(acc_o[dt][r] * inv);
+          e = max(e, exp_field(y[r]));
+        }
+        e = max_with_lane_xor32(e);
+        const int sx = max(e - 7, 0);
+        const float f = mx_inv_scale(sx);
+        sw |= (uint32_t)sx << (8 * dt);
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = dt * 32 + gi * 8 + hq * 4;
+          const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+          *reinterpret_cast<uint32_t*>(stg + col * 128 + ((((d >> 4) ^ (col & 7)) << 4) | (d & 15))) = c4;
+        }
+      }
+      if (qok && hq == 0) *reinterpret_cast<uint32_t*>(a.out_scales + qi * os_ss + h * 4) = sw;
+      uint8_t* out = reinterpret_cast<uint8_t*>(a.out) + h * a.o_hs;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int qr = it * 8 + (lane >> 3), ch = lane & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + qr * 128 + ((ch ^ (qr & 7)) << 4));
+        const int64_t qg = q0 + qr;
+        if (qg < a.Sq) *reinterpret_cast<uint4*>(out + qg * o_ss + ch * 16) = v;
+      }
+    }
+  }
+}
+
 // max over tokens of the per-head L2 norm of a [S, heads, 128] (strided) bf16 tensor
 __global__ __launch_bounds__(256) void head_max_norm_kernel(const uint16_t* x, int64_t hs, int64_t ss, int64_t S,
                                                             int heads, float* out) {
@@ -574,7 +851,18 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
   a.q_eps = qp.eps;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
   const bool rebase_k = ((Sk - 1) * k_token_stride + 128) * 2 >= (1LL << 31);
-  if (Sk <= 1024)
+  // Short key sequences of three tiles or more with queries that take no RoPE (cross-attention):
+  // up to kCrossHeadsPerGroup heads per workgroup (the largest divisor of `heads` not above it).
+  int hpw = 1;
+  if (Sk <= 1024 && Sk > 2 * BKV && qp.cos == nullptr && !rebase_k) {
+    hpw = kCrossHeadsPerGroup < heads ? kCrossHeadsPerGroup : heads;
+    while (heads % hpw) --hpw;
+  }
+  a.heads_per_group = hpw;
+  if (hpw > 1)
+    hipLaunchKernelGGL(attention_head_group_kernel, dim3(grid.x, (unsigned)(heads / hpw)), dim3(kThreads), 0,
+                       (hipStream_t)stream, a);
+  else if (Sk <= 1024)
     hipLaunchKernelGGL(HIP_KERNEL_NAME(attention_const_max_kernel<true, false>), grid, dim3(kThreads), 0,
                        (hipStream_t)stream, a);
   else if (!rebase_k)
