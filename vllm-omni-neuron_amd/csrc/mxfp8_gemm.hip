@@ -80,13 +80,15 @@ struct GemmArgs {
 };
 
 // gelu_tanh(x) = 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3);
-// hardware exp2 and reciprocal (relative error ~1e-7, far below the bf16 rounding that follows).
-// Saturates correctly: exp(-2u) -> inf gives -0/+0, exp(-2u) -> 0 gives x.
+// exp(-2u) = 2^(x (k0 + k1 x^2)) with k0 = -2 log2(e) sqrt(2/pi), k1 = 0.044715 k0 folded into one
+// polynomial; hardware exp2 and reciprocal (relative error ~1e-7, far below the bf16 rounding that
+// follows). Saturates correctly: exp(-2u) -> inf gives -0/+0, exp(-2u) -> 0 gives x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float u = x * (0.7978845608028654f + 0.035677408136300125f * (x * x));
-  const float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);  // exp(-2u) = 2^(-2u log2 e)
+  const float e = __builtin_amdgcn_exp2f(x * (-2.302208198144325f + -0.1029432395800235f * (x * x)));
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 // LDS byte offset of 16-byte chunk `chunk` of operand row `row`. The chunk index is XORed with
 // f(row) = (row & 7) ^ ((row >> 3) & 1): the 16 lanes that one LDS cycle serves read rows r..r+15
@@ -427,13 +429,18 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
         float v[16];
         epi_values<kScaled>(acc[i][j], ev, i, kScaled ? vec[768 + wm * 128 + j * 32 + r32] : 1.0f, v);
         if constexpr (EPI == WANMI_EPI_GELU_MX) {
+          // GELU rounded to bf16 two values per conversion; the block's largest exponent field is
+          // that of its largest |y|, taken as the largest (bits & 0x7fff) of the packed bf16 pairs
           float y[16];
-          int e = 0;
+          u16x2 mag = {0, 0};
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            y[q] = round_bf16(gelu_tanh(v[q]));
-            e = max(e, exp_field(y[q]));
+          for (int q = 0; q < 16; q += 2) {
+            const uint32_t p = pack_bf16x2(gelu_tanh(v[q]), gelu_tanh(v[q + 1]));
+            y[q] = bf16_lo(p);
+            y[q + 1] = bf16_hi(p);
+            mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, p & 0x7FFF7FFFu));
           }
+          int e = (int)(max(mag[0], mag[1]) >> 7);
           e = max_with_lane_xor32(e);  // lanes l and l^32 hold the two halves of the 32-block
           const int sx = max(e - 7, 0);
           const float f = mx_inv_scale(sx);
