@@ -64,14 +64,19 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 // one per-lane byte offset and the chunk offset in the scalar soffset field, so no per-chunk vector
 // address is ever materialized; descriptor extents mask the columns past H in a partial chunk.
 //
-// kLdsMod (no residual, both modulation vectors given, H <= 5120): the workgroup's four waves copy
+// kLdsMod (no residual, both modulation vectors given, H a multiple of 512 up to 5120; the block's
+// three sites): the workgroup's four waves copy
 // the fp32 mul and add vectors into LDS once (direct-to-LDS loads) and read them from there. Read
 // per row from L2 instead, the two vectors are 8 bytes per column against the row's 2 (x) + 1
 // (codes) -- four times the row's own traffic through the texture unit, the pass's busiest unit.
 // The LDS copy holds, per vector, chunk c's first four floats of every lane (lane-major, 16 bytes
 // each), then the second four, so that a lane's 16-byte reads of one chunk are consecutive across
-// lanes (bank-conflict free).
-template <int NCH, bool kLdsMod = false>
+// lanes (bank-conflict free). That instantiation also takes the norm type as a template parameter
+// (kNorm), and its rows are whole chunks: with the runtime switches the compiler computed every
+// variant of the per-value math and selected among them (five v_cndmask per value).
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+template <int NCH, bool kLdsMod = false, int kNorm = -1>
 __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float smod[kLdsMod ? 2 * 2 * NCH * 64 * 4 : 4];
@@ -90,7 +95,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
   uint32_t xp[NCH][4];  // the row's x as packed bf16 pairs (exact; also the residual sum)
 
   // ---- load (and optional gated residual add, x = bf16(h * gate + res)) ----
-  if (a.residual) {
+  if (!kLdsMod && a.residual) {
     const __amdgpu_buffer_rsrc_t r_r = rsrc(a.residual + rbase, 2 * (int64_t)H);
     const __amdgpu_buffer_rsrc_t r_ro = rsrc(a.residual_out + rbase, 2 * (int64_t)H);
     const __amdgpu_buffer_rsrc_t r_g = rsrc(a.gate, 4 * (int64_t)H);
@@ -145,9 +150,13 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
     if (!live) return;
   }
 
+  const int norm = kNorm >= 0 ? kNorm : a.norm;
+  const bool has_mul = kLdsMod || a.mul != nullptr;
+  const bool has_add = kLdsMod || a.add != nullptr;
+
   // ---- statistics (fixed-order fp32 sums, see the file header) ----
   float mu = 0.0f, rs = 1.0f;
-  if (a.norm == WANMI_NORM_LAYER) {
+  if (norm == WANMI_NORM_LAYER) {
     float s1 = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
@@ -158,10 +167,16 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
       }
     s1 = wave_sum_f32_asc(s1);
     mu = s1 / (float)H;
+    if constexpr (kNorm >= 0) {  // unpack x again below rather than hold all of it as fp32
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(xp[c][j]));
+    }
     float s2 = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const bool ok = (c < nch) && (c * 512 + lane * 8 < H);
+      const bool ok = kLdsMod || ((c < nch) && (c * 512 + lane * 8 < H));  // (kLdsMod: whole chunks)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float d0 = bf16_lo(xp[c][j]) - mu;
@@ -175,7 +190,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
     s2 = wave_sum_f32_asc(s2);
     const float var = s2 / (float)H;
     rs = (float)(1.0 / sqrt((double)var + (double)a.eps));
-  } else if (a.norm == WANMI_NORM_RMS) {
+  } else if (norm == WANMI_NORM_RMS) {
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
@@ -196,6 +211,15 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
   // Keep the per-chunk mul/add loads below the statistics: hoisted above them, all chunks' vectors
   // would be live at once (8 floats x 2 x NCH per lane) and halve occupancy.
   __builtin_amdgcn_sched_barrier(0);
+  // mu through an empty asm, so that x - mu is computed again below instead of being kept from the
+  // variance pass (the row's 8 NCH differences held in registers spilled)
+  asm volatile("" : "+v"(mu));
+  if constexpr (kNorm >= 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(xp[c][j]));
+  }
 
   // ---- normalize + modulate (+ quantize + store), one chunk at a time ----
   // y = bf16(((x - mu) * rs) * mul + add). NONE and MX finish each chunk here; ROW keeps y in xp
@@ -211,7 +235,9 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (c < nch) {
-      const bool ok = c * 512 + lane * 8 < H;
+      const bool ok = kLdsMod || c * 512 + lane * 8 < H;
+      // y as packed bf16 pairs (two values per conversion) and as fp32
+      uint32_t yp[4];
       float y[8];
       {
         float mv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
@@ -226,29 +252,39 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
           if (a.mul) load8f(r_m, lane, c, mv);
           if (a.add) load8f(r_a, lane, c, av);
         }
+        float t[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           float v = (j & 1) ? bf16_hi(xp[c][j >> 1]) : bf16_lo(xp[c][j >> 1]);
-          if (a.norm == WANMI_NORM_LAYER) {
+          if (norm == WANMI_NORM_LAYER) {
             v = (v - mu) * rs;
-          } else if (a.norm == WANMI_NORM_RMS) {
+          } else if (norm == WANMI_NORM_RMS) {
             v = v * rs;
           }
-          if (a.mul) v = v * mv[j];
-          if (a.add) v = v + av[j];
-          y[j] = ok ? round_bf16(v) : 0.0f;  // columns past H stay zero for the row reductions
+          if (has_mul) v = v * mv[j];
+          if (has_add) v = v + av[j];
+          t[j] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          yp[j] = ok ? pack_bf16x2(t[2 * j], t[2 * j + 1]) : 0u;  // columns past H stay zero
+          y[2 * j] = bf16_lo(yp[j]);
+          y[2 * j + 1] = bf16_hi(yp[j]);
         }
       }
       if (a.quant == WANMI_QUANT_NONE) {
         u32x4 ov;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ov[j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
+        for (int j = 0; j < 4; ++j) ov[j] = yp[j];
         store_b128_guarded(ov, r_o, lane * 16, c * 1024);
       } else if (a.quant == WANMI_QUANT_MX) {
         // a 32-block is 4 consecutive lanes (col / 32 == c * 16 + lane / 4)
-        int e = 0;
+        // the largest exponent field is that of the largest |y|: the largest (bits & 0x7fff) of
+        // the packed pairs
+        u16x2 mag = {0, 0};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) e = max(e, exp_field(y[j]));
+        for (int j = 0; j < 4; ++j) mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, yp[j] & 0x7FFF7FFFu));
+        int e = (int)(max(mag[0], mag[1]) >> 7);
         e = max(e, dpp_i32<0xB1>(e));  // quad_perm(1,0,3,2): lane ^ 1
         e = max(e, dpp_i32<0x4E>(e));  // quad_perm(2,3,0,1): lane ^ 2
         const int sexp = max(e - 7, 0);
@@ -262,7 +298,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(y[j]));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xp[c][j] = pack_bf16x2(y[2 * j], y[2 * j + 1]);
+        for (int j = 0; j < 4; ++j) xp[c][j] = yp[j];
       }
     }
   }
@@ -297,8 +333,13 @@ template <int NCH>
 static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.T + 3) / 4;
   if constexpr (NCH <= 10) {
-    if (!a.residual && a.mul && a.add) {
-      hipLaunchKernelGGL((adaln_quant_kernel<NCH, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    if (!a.residual && a.mul && a.add && a.H == NCH * 512) {
+      if (a.norm == WANMI_NORM_LAYER)
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      else if (a.norm == WANMI_NORM_RMS)
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_RMS>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_NONE>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
       return;
     }
   }
