@@ -65,7 +65,7 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 // address is ever materialized; descriptor extents mask the columns past H in a partial chunk.
 //
 // kLdsMod (no residual, both modulation vectors given, H a multiple of 512 up to 5120; the block's
-// three sites): the workgroup's four waves copy
+// three sites): the workgroup's eight waves (one row each) copy
 // the fp32 mul and add vectors into LDS once (direct-to-LDS loads) and read them from there. Read
 // per row from L2 instead, the two vectors are 8 bytes per column against the row's 2 (x) + 1
 // (codes) -- four times the row's own traffic through the texture unit, the pass's busiest unit.
@@ -77,14 +77,15 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 template <int NCH, bool kLdsMod = false, int kNorm = -1>
-__global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
+__global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
+  constexpr int kRows = kLdsMod ? 8 : 4;  // rows (waves) per workgroup
   __shared__ __attribute__((aligned(16))) float smod[kLdsMod ? 2 * 2 * NCH * 64 * 4 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.H;
   const int nch = a.nch;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t row = (int64_t)blockIdx.x * kRows + wave;
   const bool live = row < a.T;
   // every wave of the workgroup takes part in the vectors' copy (and its barrier); rows past T
   // load nothing (empty descriptor) and leave after it
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
     constexpr int kPerVec = 2 * NCH;  // 1 KiB loads per vector: halves x chunks
     const uint32_t base = lds_addr(smod);
     const u32x4 rm = buffer_rsrc(a.mul, 4u * (uint32_t)H), ra = buffer_rsrc(a.add, 4u * (uint32_t)H);
-    for (int k = wave; k < 2 * kPerVec; k += 4) {
+    for (int k = wave; k < 2 * kPerVec; k += kRows) {
       const int kk = k % kPerVec, hh = kk / NCH, c = kk % NCH;
       lds_dma_b128(k < kPerVec ? rm : ra, (uint32_t)(c * 512 + 8 * lane + 4 * hh) * 4, base + (uint32_t)k * 1024);
     }
@@ -332,14 +333,15 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(A
 template <int NCH>
 static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.T + 3) / 4;
+  const int64_t blocks8 = (a.T + 7) / 8;  // the LDS instantiation: eight rows per workgroup
   if constexpr (NCH <= 10) {
     if (!a.residual && a.mul && a.add && a.H == NCH * 512) {
       if (a.norm == WANMI_NORM_LAYER)
-        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER>), dim3((unsigned)blocks8), dim3(512), 0, stream, a);
       else if (a.norm == WANMI_NORM_RMS)
-        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_RMS>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_RMS>), dim3((unsigned)blocks8), dim3(512), 0, stream, a);
       else
-        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_NONE>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_NONE>), dim3((unsigned)blocks8), dim3(512), 0, stream, a);
       return;
     }
   }
