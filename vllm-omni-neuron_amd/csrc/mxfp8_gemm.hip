@@ -14,14 +14,15 @@
 // (e4m3) vectors.
 //
 // Tiling: 256 (n) x 256 (m) x 128 (k) per workgroup of 4 waves, each wave a 128 x 128 block of
-// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand codes are staged through LDS in two
-// stage buffers filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds, no VGPR round
-// trip), with a 16-byte-chunk XOR swizzle (chunk ^ (row & 7)) so the MFMA operand reads of eight
-// consecutive rows land on distinct banks. Each stage's loads are issued two stages ahead into the
-// buffer just consumed; operands are read per 64-deep slice into ping-pong registers, interleaved
-// with the MFMAs of the other slice, and a stage needs one barrier. Block scales travel four stages
-// at a time (16 bytes per row in one load, double-buffered): a row's scale bytes are 4 bytes per
-// stage, so per-stage loads would cost an address-unit pass over 64 scattered rows for every 4 bytes.
+// 4 x 4 MFMA tiles (256 fp32 accumulators per lane). Operand codes are staged through LDS by
+// direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds, no VGPR round trip), with a
+// 16-byte-chunk XOR swizzle so the MFMA operand reads of consecutive rows land on distinct banks.
+// Each stage's loads are issued two stages ahead (the weight halves on a ring of five half-stage
+// slots, the activations in two stage slots, so that a quarter of the loads can go out in the first
+// half of a stage); operands are read per 64-deep slice into ping-pong registers, interleaved with
+// the MFMAs of the other slice, and a stage needs one barrier. Block scales travel four stages at a
+// time (16 bytes per row in one load, double-buffered): a row's scale bytes are 4 bytes per stage,
+// so per-stage loads would cost an address-unit pass over 64 scattered rows for every 4 bytes.
 //
 // Measured on MI355X, these choices matter: direct-to-LDS loads with a non-zero scalar offset run
 // ~45% slower than with the whole offset in the VGPR, so the offsets are VGPR sums of a per-lane part
@@ -34,9 +35,8 @@
 // The kernel is persistent: one workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ... in an
 // order where each XCD (workgroup ids are dealt round-robin over 8 XCDs) owns a contiguous,
 // L2-friendly run of tiles grouped 4 deep along m (measured against 2, 8 and 16: 1-5% faster). The
-// next tile's first two stages and its epilogue vectors (bias, column/row scales, gate; staged in
-// LDS) are loaded while the current tile's epilogue runs, so the epilogue overlaps the next tile's
-// load latency.
+// next tile's first stage is loaded while the current tile's epilogue runs, so the epilogue overlaps
+// the next tile's load latency.
 //
 // Reference semantics: the ROW_MX projection epilogues of _qkv_cte_mx_impl / _dequant_row_mx
 // (vllm_omni_neuron/kernels/nkilib/core/qkv/qkv_cte.py:3711-3750, 3996-4021) and of the MLP
@@ -223,21 +223,16 @@ __device__ __forceinline__ DmaLanes dma_lanes(const GemmArgs& g) {
   return DmaLanes{rw + ce, rw + co, ra + ce, ra + co};
 }
 
-// kHot: the k loop's loads (one wait state, checked by the build), else the prologue's (five)
-template <bool kHot = false>
+// Row group p of both operands of stage kt into a stage buffer (weights, then activations; the
+// simple loop's layout).
 __device__ __forceinline__ void code_dma_pair(const GemmArgs& g, const TileLoads& t, const DmaLanes& dl, int kt,
                                               uint8_t* buf, int wave, int p, bool valid = true) {
   const uint32_t rg = (uint32_t)(wave * 64 + p * 8);  // first row of the row group
   const uint32_t kofs = (uint32_t)kt * BK;
   const uint32_t lds = lds_addr(buf) + rg * BK;
   const uint32_t sw = rg * (uint32_t)g.K + kofs, sa = rg * (uint32_t)g.lda + kofs;
-  if constexpr (kHot) {
-    lds_dma_b128_hot(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
-    lds_dma_b128_hot(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
-  } else {
-    lds_dma_b128(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
-    lds_dma_b128(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
-  }
+  lds_dma_b128(maybe_empty(t.w, valid), ((p & 1) ? dl.wo : dl.we) + sw, lds);
+  lds_dma_b128(maybe_empty(t.a, valid), ((p & 1) ? dl.ao : dl.ae) + sa, lds + TN * BK);
 }
 
 __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& t, int kt, uint8_t* buf, int wave,
@@ -245,40 +240,6 @@ __device__ __forceinline__ void issue_codes(const GemmArgs& g, const TileLoads& 
   const DmaLanes dl = dma_lanes(g);
 #pragma unroll
   for (int p = 0; p < 8; ++p) code_dma_pair(g, t, dl, kt, buf, wave, p, valid);
-}
-
-// One stage of the pipelined k loop is two phases of 16 MFMAs, each split into four fragment rows
-// (4 MFMAs each) with the LDS reads of one fragment row of the next slice issued before them:
-//   phase A: MFMAs on slice 0 (cur), reads of slice 1 of the same stage (nxt);
-//   phase B: MFMAs on slice 1, reads of slice 0 of the next stage, and the stage's 16 code loads, one
-//            pair after the first and third MFMA of each row.
-// Spread this way every read and load issues while an MFMA executes; issued as one block, the loads
-// would hold the wave at the texture unit's input queue (each moves 1 KiB) while its matrix pipe runs
-// dry. The scheduling barriers keep the compiler from regrouping them (it otherwise moves MFMAs
-// across the stage's barrier and clusters the reads).
-template <int I, bool kSwap>
-__device__ __forceinline__ void phase_a_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
-                                            const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
-                                            int r32, uint32_t sl) {
-  read_slice<I, I + 1>(base, sc, q, s, nxt, wn, wm, h, r32, sl);
-  __builtin_amdgcn_sched_barrier(0);
-  mfma_rows<I, I + 1, kSwap>(cur, acc);
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int I, bool kSwap>
-__device__ __forceinline__ void phase_b_row(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& nxt,
-                                            const SliceOperands& cur, f32x16 (&acc)[4][4], int wn, int wm, int h,
-                                            int r32, uint32_t sl, const GemmArgs& g, const TileLoads& t,
-                                            const DmaLanes& dl, int kt, uint8_t* buf, int wave, bool valid) {
-  read_slice<I, I + 1>(base, sc, q, s, nxt, wn, wm, h, r32, sl);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc[I][j] = mfma_tile<kSwap>(cur.w[I], cur.a[j], acc[I][j], cur.ws[I], cur.as[j]);
-    if (j == 0 || j == 2) code_dma_pair<true>(g, t, dl, kt, buf, wave, 2 * I + (j >> 1), valid);
-    __builtin_amdgcn_sched_barrier(0);
-  }
 }
 
 // Scale bytes of stage group grp (stages 4 grp .. 4 grp + 3, k-blocks [16 grp, 16 grp + 16)) ->
@@ -641,10 +602,10 @@ __device__ __forceinline__ void epilogue_vt(const GemmArgs& g, const f32x16 (&ac
   }
 }
 
-// kPipelined: the pipelined main loop (K a multiple of 512: whole scale groups, stage pairs);
-// otherwise a simple double-buffered loop that issues the next stage's loads after all reads of the
-// current one.
-template <bool kPipelined, int EPI>
+// K not a multiple of 512: a simple double-buffered loop that issues the next stage's loads after all
+// reads of the current one (the pipelined loop, mxfp8_gemm_ring_kernel below, needs whole scale
+// groups).
+template <int EPI>
 __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
   constexpr bool kSwap = EPI == kEpiVt;  // the V^T epilogue wants the transposed accumulator
@@ -666,34 +627,24 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
   // prefetches after.
   constexpr bool kPrefetchBeforeEpilogue = EPI != WANMI_EPI_GATED_RESIDUAL;
   // The epilogue stages its output in smem1, so only stage 0 of the next tile (smem0, with the
-  // first scale group and the epilogue vectors) may be loaded before or during it; stage 1 follows.
+  // first scale group and the epilogue vectors) may be loaded before or during it.
   auto prefetch0 = [&](const TileLoads& tl, float* vec) {
     issue_vectors(g, tl, vec, wave);
     issue_scales(g, tl, 0, ssc[0], wave);
     issue_codes(g, tl, 0, smem0, wave);
   };
-  auto prefetch1 = [&](const TileLoads& tl) {
-    if constexpr (kPipelined) issue_codes(g, tl, 1, smem1, wave);
-  };
 
   int v = blockIdx.x;
   init_vectors(g, svec, tid);  // published by the barrier at the top of the tile loop
   prefetch0(tile_loads(g, v), svec[0]);
-  prefetch1(tile_loads(g, v));
   int vb = 0;
 
   f32x16 acc[4][4];
   for (;;) {
     // tile state is recomputed per tile (cheap scalar work) rather than carried across the epilogue
     const TileLoads t = tile_loads(g, v);
-    // This tile's stage 0, scales and vectors have landed; in the pipelined loop stage 1 (the
-    // youngest 16 loads) may still be in flight. The partial wait is exact because loads complete in
-    // order among themselves and the previous epilogue's stores were issued either after a full wait
-    // that retired stage 0 or before stage 0 was issued.
-    if constexpr (kPipelined)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCodeLoads));
-    else
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // this tile's stage 0, scales and vectors have landed
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -702,69 +653,23 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    if constexpr (!kPipelined) {
-      for (int kt = 0; kt < KT; ++kt) {
-        uint8_t* cur = (kt & 1) ? smem1 : smem0;
-        uint8_t* nxt = (kt & 1) ? smem0 : smem1;
-        const uint32_t* sc = ssc[(kt / kScaleGroup) & 1];
-        // nobody reads nxt, nor the other scale buffer, since the last barrier
-        if (kt + 1 < KT) {
-          if ((kt + 1) % kScaleGroup == 0) issue_scales(g, t, (kt + 1) / kScaleGroup, ssc[((kt + 1) / kScaleGroup) & 1], wave);
-          issue_codes(g, t, kt + 1, nxt, wave);
-        }
-        SliceOperands op;
-        const uint32_t sl = scale_lane_offset();
-        read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32, sl);
-        mfma_rows<0, 4, kSwap>(op, acc);
-        read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32, sl);
-        mfma_rows<0, 4, kSwap>(op, acc);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      uint8_t* cur = (kt & 1) ? smem1 : smem0;
+      uint8_t* nxt = (kt & 1) ? smem0 : smem1;
+      const uint32_t* sc = ssc[(kt / kScaleGroup) & 1];
+      // nobody reads nxt, nor the other scale buffer, since the last barrier
+      if (kt + 1 < KT) {
+        if ((kt + 1) % kScaleGroup == 0) issue_scales(g, t, (kt + 1) / kScaleGroup, ssc[((kt + 1) / kScaleGroup) & 1], wave);
+        issue_codes(g, t, kt + 1, nxt, wave);
       }
-    } else {
-      // Stage s lives in smem0 for even s, smem1 for odd s; its scales in ssc[(s / 4) & 1], bytes
-      // 4 (s % 4) .. +3 of each row. Entering stage S, opA holds slice 0 of S (its reads may still
-      // be in flight). Phase A runs the slice-0 MFMAs while slice 1 of S is read into opB. Then one
-      // barrier, after this wave's reads of S and loads of S+1 are complete, certifies both that
-      // every wave is done reading S's buffer and that all of S+1 has landed. Phase B runs the slice-1
-      // MFMAs while slice 0 of S+1 is read into opA and stage S+2's codes are loaded into S's buffer,
-      // so every load has the rest of phase B and all of phase A of S+1 (16-32 MFMAs) to land. The
-      // scales of group g+1 are loaded with stage 4g+2's codes: their buffer was last read in stage
-      // 4g-1. The body has no branches (conditional issue makes the register allocator spill
-      // operands): in the last iterations the loads past the end are issued against an empty
-      // resource, which moves no data and zero-fills a buffer nobody reads again, and the slice read
-      // in the final phase B is dead.
-#define WANMI_GEMM_STAGE(S, CUR, OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                     \
-  do {                                                                                             \
-    phase_a_row<0, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<1, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<2, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    phase_a_row<3, kSwap>(CUR, SC_CUR, Q_CUR, 1, opB, opA, acc, wn, wm, h, r32, sl);                      \
-    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                   \
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));                                                     \
-    __syncthreads();                                                                               \
-    const bool more_ = (S) + 2 < KT;                                                               \
-    const int ktn_ = more_ ? (S) + 2 : 0;                                                          \
-    if (WITH_SCALES) issue_scales(g, t, ((S) + 2) / kScaleGroup, ssc[(((S) + 2) / kScaleGroup) & 1], wave, more_); \
-    phase_b_row<0, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<1, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<2, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-    phase_b_row<3, kSwap>(OTH, SC_NXT, Q_NXT, 0, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, CUR, wave, more_); \
-  } while (0)
-
-      // per-lane load and scale-read offsets, held through the k loop and dead after it
-      const DmaLanes dl = dma_lanes(g);
+      SliceOperands op;
       const uint32_t sl = scale_lane_offset();
-      SliceOperands opA, opB;
-      read_slice(smem0, ssc[0], 0, 0, opA, wn, wm, h, r32, sl);
-      for (int kt = 0; kt < KT; kt += 4) {
-        const int sg = (kt / kScaleGroup) & 1;  // this group's scale buffer; the next group's is sg ^ 1
-        WANMI_GEMM_STAGE(kt, smem0, smem1, ssc[sg], 0, ssc[sg], 1, false);
-        WANMI_GEMM_STAGE(kt + 1, smem1, smem0, ssc[sg], 1, ssc[sg], 2, false);
-        WANMI_GEMM_STAGE(kt + 2, smem0, smem1, ssc[sg], 2, ssc[sg], 3, true);
-        WANMI_GEMM_STAGE(kt + 3, smem1, smem0, ssc[sg], 3, ssc[sg ^ 1], 0, false);
-      }
-#undef WANMI_GEMM_STAGE
+      read_slice(cur, sc, kt % kScaleGroup, 0, op, wn, wm, h, r32, sl);
+      mfma_rows<0, 4, kSwap>(op, acc);
+      read_slice(cur, sc, kt % kScaleGroup, 1, op, wn, wm, h, r32, sl);
+      mfma_rows<0, 4, kSwap>(op, acc);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
     }
 
     // Every wave is past its last LDS operand read of this tile once all have passed a barrier, and
@@ -798,21 +703,323 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     if (!has_next) break;
     __syncthreads();  // every wave is done with its staging area in smem1
     if (!kPrefetchBeforeEpilogue) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
-    prefetch1(tile_loads(g, vn));
     v = vn;
     vb ^= 1;
   }
   __builtin_amdgcn_s_waitcnt(0);  // no load may still target LDS when the workgroup retires
 }
 
-template <bool kEven>
+// ------------------------------------------------------------------------------------------------
+// The pipelined k loop (K a multiple of 512), with its loads split over both phases of a stage.
+// A stage is two phases of 16 MFMAs, each split into four fragment rows (4 MFMAs each) with the LDS
+// reads of one fragment row of the next slice issued before them (phase A: MFMAs on slice 0, reads
+// of slice 1; phase B: MFMAs on slice 1, reads of slice 0 of the next stage), and the stage's loads
+// two stages ahead spread one at a time between the MFMAs; the scheduling barriers keep the compiler
+// from regrouping them (it otherwise moves MFMAs across the stage's barrier and clusters the reads).
+// All 16 of a stage's loads in phase B (the two-buffer form) asked for 64 B/clk per CU during that
+// phase, above what direct-to-LDS streaming sustains, and stretched it. LDS: the weight codes of a stage in
+// two 16 KiB halves (rows 0-127, 128-255) on a ring of five half slots, the activation codes in two
+// 32 KiB slots, the scale groups as before; 160 KiB. Half k = 2 S + h of stage S sits in half slot
+// k % 5, so the slot of stage S+2's first half (k = 2S+4) held stage S-1's second half, free since
+// the barrier of stage S-1: those 4 loads per wave go out in phase A of stage S, and stage S+2's
+// second half (the slot of stage S's first half) and its activations (stage S's activation slot),
+// 12 loads per wave, in phase B after the barrier. A wave's MFMA weight rows are one half (wn), so
+// its reads address one half slot. The epilogue vectors have no buffer of their own: at the tile's
+// last scale-group load (stage KT-2, for the group past its end) the scale loads are masked off and
+// wave w fetches vector w (bias, column scale, gate, row scale; 1 KiB each) into the scale buffer
+// that group would have used; the next tile's scale groups start in the other one.
+// ------------------------------------------------------------------------------------------------
+constexpr int kHalfBytes = 128 * BK;  // 16 KiB: 128 weight rows of one stage
+// Neutral epilogue vectors, loaded in place of an absent one: bias -0, scales and gate 1.
+#define WANMI_R8(x) x, x, x, x, x, x, x, x
+#define WANMI_R64(x) WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x)
+__device__ const float kNeutralNegZero[256] = {WANMI_R64(-0.0f), WANMI_R64(-0.0f), WANMI_R64(-0.0f), WANMI_R64(-0.0f)};
+__device__ const float kNeutralOne[256] = {WANMI_R64(1.0f), WANMI_R64(1.0f), WANMI_R64(1.0f), WANMI_R64(1.0f)};
+#undef WANMI_R64
+#undef WANMI_R8
+
+// Descriptor of wave w's epilogue vector for tile t (extent: the row scale stops at row M).
+__device__ __forceinline__ u32x4 vector_rsrc(const GemmArgs& g, const TileLoads& t, int wave) {
+  const float* p = wave == 0 ? (g.bias ? g.bias + t.n0 : kNeutralNegZero)
+                 : wave == 1 ? (g.col_scale ? g.col_scale + t.n0 : kNeutralOne)
+                 : wave == 2 ? (g.gate ? g.gate + t.n0 : kNeutralOne)
+                             : (g.row_scale ? g.row_scale + t.m0 : kNeutralOne);
+  const uint32_t bytes = (wave == 3 && g.row_scale) ? (uint32_t)(t.m_valid * 4) : 1024u;
+  return buffer_rsrc(p, bytes);
+}
+
+// A direct-to-LDS load under an all-or-nothing lane mask (exec set and restored inside the block),
+// so that a load is switched on or off without a branch. Five wait states as lds_dma_b128.
+__device__ __forceinline__ void lds_dma_b128_masked(u32x4 rsrc, uint32_t voff, uint32_t lds, bool on) {
+  uint64_t saved;
+  const uint32_t m = __builtin_amdgcn_readfirstlane(on ? ~0u : 0u);  // the same for both halves
+  asm volatile("s_mov_b64 %0, exec\n\ts_mov_b32 exec_lo, %3\n\ts_mov_b32 exec_hi, %3\n\ts_nop 4\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b64 exec, %0"
+               : "=&s"(saved)
+               : "v"(voff), "s"(rsrc), "s"(m), "{m0}"(lds)
+               : "memory");
+}
+
+// After the barrier of stage S = 4G + 2: the scales of group G + 1 (2 loads per wave) if the tile
+// has that group, else the tile's epilogue vectors (1 load per wave: vector w) into the buffer that
+// group would have used. Both are issued, one of them masked off.
+__device__ __forceinline__ void issue_scales_or_vectors(const GemmArgs& g, const TileLoads& t, int grp, uint32_t* sc,
+                                                        int wave, bool more) {
+  const uint32_t KB = (uint32_t)(g.K / 32);
+  const uint32_t lane = (uint32_t)fresh_lane_id();
+  const uint32_t v = (uint32_t)(wave * 64 + lane) * KB + (uint32_t)grp * 16;
+  const uint32_t ls = lds_addr(sc) + wave * 64 * 16;
+  lds_dma_b128_masked(t.ws, v, ls, more);
+  lds_dma_b128_masked(t.as, v, ls + TN * 16, more);
+  lds_dma_b128_masked(vector_rsrc(g, t, wave), lane * 16, lds_addr(sc) + wave * 1024, !more);
+}
+constexpr int kActBytes = TM * BK;    // 32 KiB: 256 token rows of one stage
+
+// Fragments [I0, I1) of slice s: weight rows i * 32 + r32 of the wave's half (wbase), token rows
+// wm * 128 + i * 32 + r32 (abase). Same lane data and scale bytes as read_slice.
+template <int I0 = 0, int I1 = 4>
+__device__ __forceinline__ void read_slice_r(const uint8_t* wbase, const uint8_t* abase, const uint32_t* sc, int q,
+                                             int s, SliceOperands& op, int wn, int wm, int h, int r32, uint32_t sl) {
+  const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
+  const uint8_t* scb = reinterpret_cast<const uint8_t*>(sc) + 4 * q + 2 * s;
+  const uint8_t* scw = scb + wn * 128 * 16 + sl;
+  const uint8_t* sca = scb + (TN + wm * 128) * 16 + sl;
+#pragma unroll
+  for (int i = I0; i < I1; ++i) {
+    const int rw = i * 32 + r32;
+    const uint4 x0 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c0));
+    const uint4 x1 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c1));
+    op.w[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    const int ra = wm * 128 + i * 32 + r32;
+    const uint4 y0 = *reinterpret_cast<const uint4*>(abase + swz(ra, c0));
+    const uint4 y1 = *reinterpret_cast<const uint4*>(abase + swz(ra, c1));
+    op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
+    op.ws[i] = (int)scw[i * 32 * 16];
+    op.as[i] = (int)sca[i * 32 * 16];
+  }
+}
+
+// One direct-to-LDS load of weight half hh, row group p (rows 128 hh + 8 p .. + 7) of stage kt into
+// the half slot at `dst`; of activation row group p (rows 8 p .. + 7) into the slot at `dst`.
+template <bool kHot>
+__device__ __forceinline__ void w_half_dma(const GemmArgs& g, const TileLoads& t, const DmaLanes& dl, int kt, int hh,
+                                           int p, uint32_t dst, bool valid) {
+  const uint32_t off = ((p & 1) ? dl.wo : dl.we) + (uint32_t)(128 * hh + 8 * p) * (uint32_t)g.K + (uint32_t)kt * BK;
+  if constexpr (kHot)
+    lds_dma_b128_hot(maybe_empty(t.w, valid), off, dst + (uint32_t)(8 * p * BK));
+  else
+    lds_dma_b128(maybe_empty(t.w, valid), off, dst + (uint32_t)(8 * p * BK));
+}
+template <bool kHot>
+__device__ __forceinline__ void act_dma(const GemmArgs& g, const TileLoads& t, const DmaLanes& dl, int kt, int p,
+                                        uint32_t dst, bool valid) {
+  const uint32_t off = ((p & 1) ? dl.ao : dl.ae) + (uint32_t)(8 * p) * (uint32_t)g.lda + (uint32_t)kt * BK;
+  if constexpr (kHot)
+    lds_dma_b128_hot(maybe_empty(t.a, valid), off, dst + (uint32_t)(8 * p * BK));
+  else
+    lds_dma_b128(maybe_empty(t.a, valid), off, dst + (uint32_t)(8 * p * BK));
+}
+
+// All 16 loads of stage kt outside the k loop: wave w takes weight row groups 4w .. 4w+3 of both
+// halves and activation row groups 8w .. 8w+7.
+__device__ __forceinline__ void issue_stage_r(const GemmArgs& g, const TileLoads& t, int kt, uint32_t h0, uint32_t h1,
+                                              uint32_t act, int wave) {
+  const DmaLanes dl = dma_lanes(g);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w_half_dma<false>(g, t, dl, kt, 0, 4 * wave + i, h0, true);
+    w_half_dma<false>(g, t, dl, kt, 1, 4 * wave + i, h1, true);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) act_dma<false>(g, t, dl, kt, 8 * wave + i, act, true);
+}
+
+// Phase A row I: reads of slice 1 of the stage, 4 MFMAs, and weight row group 4w + I of half 0 of
+// stage kt (two stages ahead) after the first MFMA.
+template <int I, bool kSwap>
+__device__ __forceinline__ void phase_a_row_r(const uint8_t* wb, const uint8_t* ab, const uint32_t* sc, int q,
+                                              SliceOperands& nxt, const SliceOperands& cur, f32x16 (&acc)[4][4], int wn,
+                                              int wm, int h, int r32, uint32_t sl, const GemmArgs& g,
+                                              const TileLoads& t, const DmaLanes& dl, int kt, uint32_t h0, int wave,
+                                              bool valid) {
+  read_slice_r<I, I + 1>(wb, ab, sc, q, 1, nxt, wn, wm, h, r32, sl);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[I][j] = mfma_tile<kSwap>(cur.w[I], cur.a[j], acc[I][j], cur.ws[I], cur.as[j]);
+    if (j == 0) w_half_dma<true>(g, t, dl, kt, 0, 4 * wave + I, h0, valid);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Phase B row I: reads of slice 0 of the next stage, 4 MFMAs, and three loads of stage kt: weight
+// row group 4w + I of half 1 and activation row groups 8w + 2I, 8w + 2I + 1.
+template <int I, bool kSwap>
+__device__ __forceinline__ void phase_b_row_r(const uint8_t* wb, const uint8_t* ab, const uint32_t* sc, int q,
+                                              SliceOperands& nxt, const SliceOperands& cur, f32x16 (&acc)[4][4], int wn,
+                                              int wm, int h, int r32, uint32_t sl, const GemmArgs& g,
+                                              const TileLoads& t, const DmaLanes& dl, int kt, uint32_t h1,
+                                              uint32_t act, int wave, bool valid) {
+  read_slice_r<I, I + 1>(wb, ab, sc, q, 0, nxt, wn, wm, h, r32, sl);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[I][j] = mfma_tile<kSwap>(cur.w[I], cur.a[j], acc[I][j], cur.ws[I], cur.as[j]);
+    if (j == 0) w_half_dma<true>(g, t, dl, kt, 1, 4 * wave + I, h1, valid);
+    if (j == 1) act_dma<true>(g, t, dl, kt, 8 * wave + 2 * I, act, valid);
+    if (j == 2) act_dma<true>(g, t, dl, kt, 8 * wave + 2 * I + 1, act, valid);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void mxfp8_gemm_ring_kernel(GemmArgs g) {
+#pragma clang fp contract(off)
+  constexpr bool kSwap = EPI == kEpiVt;
+  __shared__ __attribute__((aligned(16))) uint8_t sWh[5][kHalfBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t sAct[2][kActBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t ssc[2][2 * 256 * 4];  // scale groups; the tile's vectors at its end
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave >> 1, wm = wave & 1;
+  const int h = lane >> 5;
+  const int r32 = lane & 31;
+  const int KT = (int)(g.K / BK);  // a multiple of 4
+  const int total = g.tiles_m * g.tiles_n;
+  constexpr bool kPrefetchBeforeEpilogue = EPI != WANMI_EPI_GATED_RESIDUAL;
+  auto hs = [&](int k) { return lds_addr(sWh[k % 5]); };
+  // Each tile starts with stage 0's halves in slots 0, 1 and stage 1's in 2, 3; activations of
+  // stage S in slot S % 2. Scale group G of a tile uses buffer (G + par) & 1.
+  auto prefetch0 = [&](const TileLoads& tl, int par) {
+    issue_scales(g, tl, 0, ssc[par & 1], wave);
+    issue_stage_r(g, tl, 0, hs(0), hs(1), lds_addr(sAct[0]), wave);
+  };
+  auto prefetch1 = [&](const TileLoads& tl) { issue_stage_r(g, tl, 1, hs(2), hs(3), lds_addr(sAct[1]), wave); };
+
+  int v = blockIdx.x;
+  int par = 0;
+  prefetch0(tile_loads(g, v), par);
+  prefetch1(tile_loads(g, v));
+
+  f32x16 acc[4][4];
+  for (;;) {
+    const TileLoads t = tile_loads(g, v);
+    const int vpar = ((KT >> 2) + par) & 1;  // scale buffer that takes this tile's epilogue vectors
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCodeLoads));
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Entering stage S, opA holds slice 0 of S. Phase A: slice-0 MFMAs, slice-1 reads of S, stage
+    // S+2's first weight half loaded. Barrier after this wave's reads of S and its loads of S+1 are
+    // complete (outstanding: the 4 loads just issued). Phase B: slice-1 MFMAs, slice-0 reads of S+1,
+    // stage S+2's second weight half and activations loaded. After the barrier of stage 4G+2 the
+    // scales of group G+1, or at the tile's last group its epilogue vectors.
+#define WANMI_GEMM_RSTAGE(S, ACT_CUR, ACT_OTH, SC_CUR, Q_CUR, SC_NXT, Q_NXT, WITH_SCALES)                      \
+  do {                                                                                                  \
+    const int k0_ = 2 * (S);                                                                            \
+    const bool more_ = (S) + 2 < KT;                                                                    \
+    const int ktn_ = more_ ? (S) + 2 : 0;                                                               \
+    const uint8_t* wcur_ = sWh[(k0_ + wn) % 5];                                                         \
+    const uint8_t* wnxt_ = sWh[(k0_ + 2 + wn) % 5];                                                     \
+    const uint32_t h0_ = hs(k0_ + 4), h1_ = hs(k0_ + 5);                                                \
+    phase_a_row_r<0, kSwap>(wcur_, ACT_CUR, SC_CUR, Q_CUR, opB, opA, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h0_, wave, more_); \
+    phase_a_row_r<1, kSwap>(wcur_, ACT_CUR, SC_CUR, Q_CUR, opB, opA, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h0_, wave, more_); \
+    phase_a_row_r<2, kSwap>(wcur_, ACT_CUR, SC_CUR, Q_CUR, opB, opA, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h0_, wave, more_); \
+    phase_a_row_r<3, kSwap>(wcur_, ACT_CUR, SC_CUR, Q_CUR, opB, opA, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h0_, wave, more_); \
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));                                                        \
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));                                                          \
+    __syncthreads();                                                                                    \
+    if (WITH_SCALES)                                                                                    \
+      issue_scales_or_vectors(g, t, ((S) + 2) / kScaleGroup, ssc[((((S) + 2) / kScaleGroup) + par) & 1], wave, more_); \
+    phase_b_row_r<0, kSwap>(wnxt_, ACT_OTH, SC_NXT, Q_NXT, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h1_, lds_addr(ACT_CUR), wave, more_); \
+    phase_b_row_r<1, kSwap>(wnxt_, ACT_OTH, SC_NXT, Q_NXT, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h1_, lds_addr(ACT_CUR), wave, more_); \
+    phase_b_row_r<2, kSwap>(wnxt_, ACT_OTH, SC_NXT, Q_NXT, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h1_, lds_addr(ACT_CUR), wave, more_); \
+    phase_b_row_r<3, kSwap>(wnxt_, ACT_OTH, SC_NXT, Q_NXT, opA, opB, acc, wn, wm, h, r32, sl, g, t, dl, ktn_, h1_, lds_addr(ACT_CUR), wave, more_); \
+  } while (0)
+
+    {
+      const DmaLanes dl = dma_lanes(g);
+      const uint32_t sl = scale_lane_offset();
+      SliceOperands opA, opB;
+      read_slice_r(sWh[wn], sAct[0], ssc[par & 1], 0, 0, opA, wn, wm, h, r32, sl);
+      for (int kt = 0; kt < KT; kt += 4) {
+        const int sg = ((kt / kScaleGroup) + par) & 1;
+        WANMI_GEMM_RSTAGE(kt, sAct[0], sAct[1], ssc[sg], 0, ssc[sg], 1, false);
+        WANMI_GEMM_RSTAGE(kt + 1, sAct[1], sAct[0], ssc[sg], 1, ssc[sg], 2, false);
+        WANMI_GEMM_RSTAGE(kt + 2, sAct[0], sAct[1], ssc[sg], 2, ssc[sg], 3, true);
+        WANMI_GEMM_RSTAGE(kt + 3, sAct[1], sAct[0], ssc[sg], 3, ssc[sg ^ 1], 0, false);
+      }
+    }
+#undef WANMI_GEMM_RSTAGE
+
+    // Every wave is past its last LDS read of the tile after a barrier, and the loads past the end
+    // of K and the vectors are complete after vmcnt(0). The next tile's stage 0 then goes to half
+    // slots 0-1 and activation slot 0, its first scale group to the buffer the vectors are not in;
+    // the epilogue stages waves 0-1 in activation slot 1 and waves 2-3 in half slots 2-3, where the
+    // next tile's stage 1 is loaded after it.
+    const float* vec = reinterpret_cast<const float*>(ssc[vpar]);
+    const int m0 = (int)t.m0, n0 = (int)t.n0;
+    const int vn = v + (int)gridDim.x;
+    const bool has_next = vn < total;
+    const int par_n = vpar ^ 1;
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    if (kPrefetchBeforeEpilogue && has_next) prefetch0(tile_loads(g, vn), par_n);
+    {
+      uint8_t* stage = wave < 2 ? sAct[1] + wave * kStageWave : sWh[wave];
+      const bool scaled = g.row_scale || g.col_scale;
+      if constexpr (EPI == kEpiVt) {
+        if (scaled) epilogue_vt<true>(g, acc, vec, stage, m0, n0, wm, wn);
+        else epilogue_vt<false>(g, acc, vec, stage, m0, n0, wm, wn);
+      } else if constexpr (EPI == WANMI_EPI_BF16) {
+        if (g.row_sumsq) {
+          if (scaled) epilogue<EPI, true, true>(g, acc, vec, stage, m0, n0, wm, wn);
+          else epilogue<EPI, false, true>(g, acc, vec, stage, m0, n0, wm, wn);
+        } else {
+          if (scaled) epilogue<EPI, true, false>(g, acc, vec, stage, m0, n0, wm, wn);
+          else epilogue<EPI, false, false>(g, acc, vec, stage, m0, n0, wm, wn);
+        }
+      } else {
+        if (scaled) epilogue<EPI, true, false>(g, acc, vec, stage, m0, n0, wm, wn);
+        else epilogue<EPI, false, false>(g, acc, vec, stage, m0, n0, wm, wn);
+      }
+    }
+    if (!has_next) break;
+    __syncthreads();  // every wave is done with its staging area and the vectors
+    if (!kPrefetchBeforeEpilogue) prefetch0(tile_loads(g, vn), par_n);
+    prefetch1(tile_loads(g, vn));
+    v = vn;
+    par = par_n;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load may still target LDS when the workgroup retires
+}
+
+// kPipelined (K a multiple of 512): the pipelined ring kernel; otherwise the simple loop.
+template <bool kPipelined>
 static void launch_gemm(int epilogue, dim3 grid, hipStream_t stream, const GemmArgs& g) {
-  switch (epilogue) {
-    case WANMI_EPI_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_BF16>), grid, dim3(256), 0, stream, g); break;
-    case WANMI_EPI_GELU_MX: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_MX>), grid, dim3(256), 0, stream, g); break;
-    case WANMI_EPI_GELU_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GELU_BF16>), grid, dim3(256), 0, stream, g); break;
-    case kEpiVt: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, kEpiVt>), grid, dim3(256), 0, stream, g); break;
-    default: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEven, WANMI_EPI_GATED_RESIDUAL>), grid, dim3(256), 0, stream, g); break;
+  if constexpr (kPipelined) {
+    switch (epilogue) {
+      case WANMI_EPI_BF16: hipLaunchKernelGGL((mxfp8_gemm_ring_kernel<WANMI_EPI_BF16>), grid, dim3(256), 0, stream, g); break;
+      case WANMI_EPI_GELU_MX: hipLaunchKernelGGL((mxfp8_gemm_ring_kernel<WANMI_EPI_GELU_MX>), grid, dim3(256), 0, stream, g); break;
+      case WANMI_EPI_GELU_BF16: hipLaunchKernelGGL((mxfp8_gemm_ring_kernel<WANMI_EPI_GELU_BF16>), grid, dim3(256), 0, stream, g); break;
+      case kEpiVt: hipLaunchKernelGGL((mxfp8_gemm_ring_kernel<kEpiVt>), grid, dim3(256), 0, stream, g); break;
+      default: hipLaunchKernelGGL((mxfp8_gemm_ring_kernel<WANMI_EPI_GATED_RESIDUAL>), grid, dim3(256), 0, stream, g); break;
+    }
+  } else {
+    switch (epilogue) {
+      case WANMI_EPI_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<WANMI_EPI_BF16>), grid, dim3(256), 0, stream, g); break;
+      case WANMI_EPI_GELU_MX: hipLaunchKernelGGL((mxfp8_gemm_kernel<WANMI_EPI_GELU_MX>), grid, dim3(256), 0, stream, g); break;
+      case WANMI_EPI_GELU_BF16: hipLaunchKernelGGL((mxfp8_gemm_kernel<WANMI_EPI_GELU_BF16>), grid, dim3(256), 0, stream, g); break;
+      case kEpiVt: hipLaunchKernelGGL((mxfp8_gemm_kernel<kEpiVt>), grid, dim3(256), 0, stream, g); break;
+      default: hipLaunchKernelGGL((mxfp8_gemm_kernel<WANMI_EPI_GATED_RESIDUAL>), grid, dim3(256), 0, stream, g); break;
+    }
   }
 }
 
