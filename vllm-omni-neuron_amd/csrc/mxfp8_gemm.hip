@@ -114,32 +114,39 @@ __device__ __forceinline__ uint32_t scale_lane_offset() {
   return (l & 31) * 16 + (l >> 5);
 }
 
-// Reads fragments [I0, I1) of slice s (0 or 1) of an LDS stage. Lane data: bytes 0-15 =
-// k[64s + 16h, +16), bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of
-// its row, byte 4q + 2s + h (q = the stage's position in its scale group) of the row's 16 scale bytes
-// in `sc` ([2][256] x 16 B: W rows, then A rows), read as a byte so the MFMA takes it as is.
+// Reads fragments [I0, I1) of slice s (0 or 1): weight rows i * 32 + r32 of the wave's 128-row half
+// (wbase) and token rows wm * 128 + i * 32 + r32 (abase). Lane data: bytes 0-15 = k[64s + 16h, +16),
+// bytes 16-31 = k[64s + 32 + 16h, +16); the lane's scale byte is block 2s + h of its row, byte
+// 4q + 2s + h (q = the stage's position in its scale group) of the row's 16 scale bytes in `sc`
+// ([2][256] x 16 B: W rows, then A rows), read as a byte so the MFMA takes it as is. The swizzle
+// repeats every 16 rows, so a half read at its own base matches the whole stage read at row 128 wn.
 template <int I0 = 0, int I1 = 4>
-__device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& op,
-                                           int wn, int wm, int h, int r32, uint32_t sl) {
-  const uint8_t* sw = base;
-  const uint8_t* sa = base + TN * BK;
+__device__ __forceinline__ void read_slice_r(const uint8_t* wbase, const uint8_t* abase, const uint32_t* sc, int q,
+                                             int s, SliceOperands& op, int wn, int wm, int h, int r32, uint32_t sl) {
   const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
   const uint8_t* scb = reinterpret_cast<const uint8_t*>(sc) + 4 * q + 2 * s;
   const uint8_t* scw = scb + wn * 128 * 16 + sl;
   const uint8_t* sca = scb + (TN + wm * 128) * 16 + sl;
 #pragma unroll
   for (int i = I0; i < I1; ++i) {
-    const int rw = wn * 128 + i * 32 + r32;
-    const uint4 x0 = *reinterpret_cast<const uint4*>(sw + swz(rw, c0));
-    const uint4 x1 = *reinterpret_cast<const uint4*>(sw + swz(rw, c1));
+    const int rw = i * 32 + r32;
+    const uint4 x0 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c0));
+    const uint4 x1 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c1));
     op.w[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
     const int ra = wm * 128 + i * 32 + r32;
-    const uint4 y0 = *reinterpret_cast<const uint4*>(sa + swz(ra, c0));
-    const uint4 y1 = *reinterpret_cast<const uint4*>(sa + swz(ra, c1));
+    const uint4 y0 = *reinterpret_cast<const uint4*>(abase + swz(ra, c0));
+    const uint4 y1 = *reinterpret_cast<const uint4*>(abase + swz(ra, c1));
     op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
     op.ws[i] = (int)scw[i * 32 * 16];
     op.as[i] = (int)sca[i * 32 * 16];
   }
+}
+
+// The same from one stage buffer (weight rows, then token rows).
+template <int I0 = 0, int I1 = 4>
+__device__ __forceinline__ void read_slice(const uint8_t* base, const uint32_t* sc, int q, int s, SliceOperands& op,
+                                           int wn, int wm, int h, int r32, uint32_t sl) {
+  read_slice_r<I0, I1>(base + wn * 128 * BK, base + TN * BK, sc, q, s, op, wn, wm, h, r32, sl);
 }
 
 // One MFMA of weight fragment i against token fragment j. kSwap puts the tokens in the A operand,
@@ -717,9 +724,9 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 // two stages ahead spread one at a time between the MFMAs; the scheduling barriers keep the compiler
 // from regrouping them (it otherwise moves MFMAs across the stage's barrier and clusters the reads).
 // All 16 of a stage's loads in phase B (the two-buffer form) asked for 64 B/clk per CU during that
-// phase, above what direct-to-LDS streaming sustains, and stretched it. LDS: the weight codes of a stage in
-// two 16 KiB halves (rows 0-127, 128-255) on a ring of five half slots, the activation codes in two
-// 32 KiB slots, the scale groups as before; 160 KiB. Half k = 2 S + h of stage S sits in half slot
+// phase, above what direct-to-LDS streaming sustains, and stretched it.
+// LDS: the weight codes of a stage in two 16 KiB halves (rows 0-127, 128-255) on a ring of five half
+// slots, the activation codes in two 32 KiB slots, the scale groups as before; 160 KiB. Half k = 2 S + h of stage S sits in half slot
 // k % 5, so the slot of stage S+2's first half (k = 2S+4) held stage S-1's second half, free since
 // the barrier of stage S-1: those 4 loads per wave go out in phase A of stage S, and stage S+2's
 // second half (the slot of stage S's first half) and its activations (stage S's activation slot),
@@ -730,6 +737,7 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
 // that group would have used; the next tile's scale groups start in the other one.
 // ------------------------------------------------------------------------------------------------
 constexpr int kHalfBytes = 128 * BK;  // 16 KiB: 128 weight rows of one stage
+constexpr int kActBytes = TM * BK;    // 32 KiB: 256 token rows of one stage
 // Neutral epilogue vectors, loaded in place of an absent one: bias -0, scales and gate 1.
 #define WANMI_R8(x) x, x, x, x, x, x, x, x
 #define WANMI_R64(x) WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x), WANMI_R8(x)
@@ -752,7 +760,7 @@ __device__ __forceinline__ u32x4 vector_rsrc(const GemmArgs& g, const TileLoads&
 // so that a load is switched on or off without a branch. Five wait states as lds_dma_b128.
 __device__ __forceinline__ void lds_dma_b128_masked(u32x4 rsrc, uint32_t voff, uint32_t lds, bool on) {
   uint64_t saved;
-  const uint32_t m = __builtin_amdgcn_readfirstlane(on ? ~0u : 0u);  // the same for both halves
+  const uint32_t m = __builtin_amdgcn_readfirstlane(on ? ~0u : 0u);  // exec_lo and exec_hi alike
   asm volatile("s_mov_b64 %0, exec\n\ts_mov_b32 exec_lo, %3\n\ts_mov_b32 exec_hi, %3\n\ts_nop 4\n\t"
                "buffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b64 exec, %0"
                : "=&s"(saved)
@@ -772,31 +780,6 @@ __device__ __forceinline__ void issue_scales_or_vectors(const GemmArgs& g, const
   lds_dma_b128_masked(t.ws, v, ls, more);
   lds_dma_b128_masked(t.as, v, ls + TN * 16, more);
   lds_dma_b128_masked(vector_rsrc(g, t, wave), lane * 16, lds_addr(sc) + wave * 1024, !more);
-}
-constexpr int kActBytes = TM * BK;    // 32 KiB: 256 token rows of one stage
-
-// Fragments [I0, I1) of slice s: weight rows i * 32 + r32 of the wave's half (wbase), token rows
-// wm * 128 + i * 32 + r32 (abase). Same lane data and scale bytes as read_slice.
-template <int I0 = 0, int I1 = 4>
-__device__ __forceinline__ void read_slice_r(const uint8_t* wbase, const uint8_t* abase, const uint32_t* sc, int q,
-                                             int s, SliceOperands& op, int wn, int wm, int h, int r32, uint32_t sl) {
-  const int c0 = s * 4 + h, c1 = s * 4 + 2 + h;
-  const uint8_t* scb = reinterpret_cast<const uint8_t*>(sc) + 4 * q + 2 * s;
-  const uint8_t* scw = scb + wn * 128 * 16 + sl;
-  const uint8_t* sca = scb + (TN + wm * 128) * 16 + sl;
-#pragma unroll
-  for (int i = I0; i < I1; ++i) {
-    const int rw = i * 32 + r32;
-    const uint4 x0 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c0));
-    const uint4 x1 = *reinterpret_cast<const uint4*>(wbase + swz(rw, c1));
-    op.w[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-    const int ra = wm * 128 + i * 32 + r32;
-    const uint4 y0 = *reinterpret_cast<const uint4*>(abase + swz(ra, c0));
-    const uint4 y1 = *reinterpret_cast<const uint4*>(abase + swz(ra, c1));
-    op.a[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w, (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
-    op.ws[i] = (int)scw[i * 32 * 16];
-    op.as[i] = (int)sca[i * 32 * 16];
-  }
 }
 
 // One direct-to-LDS load of weight half hh, row group p (rows 128 hh + 8 p .. + 7) of stage kt into
