@@ -34,6 +34,20 @@ def test_abi_version_and_error_reporting(pkg):
     assert b"multiple of 32" in lib.wanmi_last_error()
 
 
+def test_missing_library_raises(pkg, monkeypatch, tmp_path):
+    """Without the built library every op fails loudly; nothing falls back to the CPU."""
+    import pytest
+    import torch
+
+    lib_mod = pkg._lib
+    monkeypatch.setattr(lib_mod, "_LIB", None)
+    monkeypatch.setattr(lib_mod, "LIB_PATH", tmp_path / "libwanmi.so")
+    with pytest.raises(RuntimeError, match="is missing"):
+        lib_mod.load()
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.adaln_modulate(torch.zeros(4, 64, dtype=torch.bfloat16), eps=1e-6)
+
+
 def test_cpu_tensor_is_rejected(pkg):
     import pytest
     import torch
