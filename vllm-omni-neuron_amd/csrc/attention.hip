@@ -175,8 +175,20 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = blockIdx.y;
-  const int64_t q0 = (int64_t)blockIdx.x * BQ + wave * 32;
+  // Workgroups go to the 8 XCDs round-robin by linear index. With the heads a multiple of 8, XCD x
+  // takes heads x * heads/8 .. + heads/8 - 1 whole, query block after query block, so that all of
+  // its CUs stream the same head's K/V tiles through its L2 instead of every XCD fetching every head
+  // (the same (head, query block) pairs, each computed as before).
+  int hb = blockIdx.y, qb = blockIdx.x;
+  if ((gridDim.y & 7) == 0) {
+    const int nq = (int)gridDim.x;
+    const int L = (int)blockIdx.x + (int)blockIdx.y * nq;
+    const int k = L >> 3;
+    hb = (L & 7) * (int)(gridDim.y >> 3) + k / nq;
+    qb = k % nq;
+  }
+  const int h = hb;
+  const int64_t q0 = (int64_t)qb * BQ + wave * 32;
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int hq = lane >> 5;
 
