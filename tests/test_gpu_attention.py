@@ -35,9 +35,12 @@ def _check_attn(out, ref):
 # key counts cover 1, 2, 3, 4, 5, 7 and 8 tiles of 64 (the K/V ring loads two tiles per barrier, so
 # odd and even tile counts and a partial last tile take different paths). With 3 to 16 tiles and
 # more than one head, a workgroup walks several heads (2, 3, 4 or 5 per group here, the last two with
-# several groups: 12 heads in three groups of 4 over a last tile of one key, 10 in two of 5).
+# several groups: 12 heads in three groups of 4 over a last tile of one key, 10 in two of 5). With
+# the heads a multiple of 8 the one-head-per-workgroup kernels place whole heads per XCD: 8 heads
+# over 2 tiles (the short-key kernel) and 16 over 18 tiles.
 @pytest.mark.parametrize("Sq,Sk,N", [(1, 1, 1), (300, 200, 2), (129, 197, 3), (64, 512, 4), (96, 100, 2),
-                                     (70, 150, 1), (40, 300, 1), (33, 448, 1), (1000, 129, 12), (513, 512, 10)])
+                                     (70, 150, 1), (40, 300, 1), (33, 448, 1), (1000, 129, 12), (513, 512, 10),
+                                     (300, 100, 8), (200, 1100, 16)])
 def test_attention_core_small(pkg, dev, Sq, Sk, N):
     ops = pkg.attention_ops
     q, k, v = _rand((Sq, N, 128), 1), _rand((Sk, N, 128), 2), _rand((Sk, N, 128), 3)
