@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   // before every LDS read); the loop waits for them itself.
   const int k_row = lane >> 4, k_pc = lane & 15;
   const int v_row = lane >> 3, v_pc = lane & 7;
-  auto issue_tile = [&](int kt) {
+  auto issue_tile_k = [&](int kt) {
     const int b = kt % kStages;
     const int64_t kbase = (int64_t)kt * BKV;
     // The tile's key offset stays in the per-lane offset (soffset is not range-checked), so that
@@ -222,13 +222,21 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
       const int c = k_pc ^ (key & 15);
       lds_dma_b128_hot(r_k, (uint32_t)(((key0 + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
     }
+  };
+  auto issue_tile_v = [&](int kt) {
+    const int b = kt % kStages;
+    const int64_t kbase = (int64_t)kt * BKV;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int d = wave * 16 + i * 8 + v_row;
       const int c = v_pc ^ (d & 7) ^ ((d >> 3) & 1);
       lds_dma_b128_hot(r_v, (uint32_t)((d * a.vt_ld + c * 8) * 2), (uint32_t)(kbase * 2),
-                   lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
+                       lds_addr(sV[b] + (wave * 16 + i * 8) * 128));
     }
+  };
+  auto issue_tile = [&](int kt) {
+    issue_tile_k(kt);
+    issue_tile_v(kt);
   };
   const int ntiles = (int)((a.Sk + BKV - 1) / BKV);
   // The first three tiles go out before anything else, so their latency overlaps the Q loads.
@@ -376,13 +384,23 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     pipeline_step<false, kShortKV>(sK[0], 1, sV[0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
   // Tile t of the steady state (1 <= t < ntiles - 1): outstanding loads are tiles t and t+1 (four
   // per wave each); wait for tile t, publish it, refill tile t-2's slot with tile t+2, then the two
-  // pipeline steps of t (`slot` = t % kStages).
+  // pipeline steps of t (`slot` = t % kStages). Tile t+2's K goes out after the barrier and its V^T
+  // between the two steps, so that the eight waves' loads reach the texture unit in two bursts
+  // rather than one that every wave waits behind. The first step runs at wave priority 1 and the
+  // second at 0: the two waves of a SIMD start the tile together and the older one, favoured by the
+  // arbiter, gets ahead; a wave still in its first step then wins over one already in its second,
+  // which keeps the pair near each other, one's exps beside the other's MFMAs, rather than the
+  // older one idling at the next barrier while the younger finishes alone. Loads and results are
+  // those of the unpartitioned tile (bit-identical).
   auto steady_tile = [&](int t, int slot) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
     __syncthreads();
-    if (t + 2 < ntiles) issue_tile(t + 2);
+    if (t + 2 < ntiles) issue_tile_k(t + 2);
     const int prev = (slot + kStages - 1) % kStages;
+    __builtin_amdgcn_s_setprio(1);
     pipeline_step<false, kShortKV>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    __builtin_amdgcn_s_setprio(0);
+    if (t + 2 < ntiles) issue_tile_v(t + 2);
     pipeline_step<false, kShortKV>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
   };
   for (int t = 1; t < ntiles - 1; ++t) steady_tile(t, t % kStages);
