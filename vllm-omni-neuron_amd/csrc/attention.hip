@@ -515,18 +515,21 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
   const int v_row = lane >> 3, v_pc = lane & 7;
   // Tile kt of the group's head hl into slot (hl * ntiles + kt) % kStages; same lane mapping and
   // descriptors as attention_const_max_kernel, built per tile from the head.
-  auto issue_tile = [&](int hl, int kt) {
+  auto issue_tile = [&](int hl, int kt, int part = 0) {  // part: 0 both, 1 K only, 2 V^T only
     const int b = (hl * ntiles + kt) % kStages;
     const int hd = h_first + hl;
     const u32x4 r_k = buffer_rsrc(a.k + hd * a.k_hs, (uint32_t)(((a.Sk - 1) * a.k_ss + 128) * 2));
     const u32x4 r_v = buffer_rsrc(a.vt + (int64_t)hd * 128 * a.vt_ld, (uint32_t)(128 * a.vt_ld * 2));
     const int64_t kbase = (int64_t)kt * BKV;
+    if (part != 2) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int key = wave * 8 + i * 4 + k_row;
-      const int c = k_pc ^ (key & 15);
-      lds_dma_b128_hot(r_k, (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+      for (int i = 0; i < 2; ++i) {
+        const int key = wave * 8 + i * 4 + k_row;
+        const int c = k_pc ^ (key & 15);
+        lds_dma_b128_hot(r_k, (uint32_t)(((kbase + key) * a.k_ss + c * 8) * 2), lds_addr(sK[b] + (wave * 8 + i * 4) * 256));
+      }
     }
+    if (part == 1) return;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int d = wave * 16 + i * 8 + v_row;
@@ -536,13 +539,13 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
     }
   };
   // tile g + 2 of tile g = (hl, kt), if the group has one (ntiles >= 3: at most one wrap)
-  auto issue_ahead = [&](int hl, int kt) {
+  auto issue_ahead = [&](int hl, int kt, int part = 0) {
     int kt2 = kt + 2, hl2 = hl;
     if (kt2 >= ntiles) {
       kt2 -= ntiles;
       ++hl2;
     }
-    if (hl2 < hpw) issue_tile(hl2, kt2);
+    if (hl2 < hpw) issue_tile(hl2, kt2, part);
   };
   issue_tile(0, 0);
   issue_tile(0, 1);
@@ -656,14 +659,19 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
     const int s0 = g0 % kStages;
     f32x16 s_prev = qk_half(sK[s0], 0, qf, negc, col, hq);
     pipeline_step<false, true>(sK[s0], 1, sV[s0], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
-    // steady tiles: outstanding are tiles g and g + 1 (four loads per wave each)
+    // steady tiles: outstanding are tiles g and g + 1 (four loads per wave each); as in
+    // attention_const_max_kernel, tile g + 2's K goes out after the barrier and its V^T between the
+    // steps, and the first step runs at wave priority 1
     for (int t = 1; t < ntiles - 1; ++t) {
       const int slot = (g0 + t) % kStages;
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
       __syncthreads();
-      issue_ahead(hl, t);
+      issue_ahead(hl, t, 1);
       const int prev = (slot + kStages - 1) % kStages;
+      __builtin_amdgcn_s_setprio(1);
       pipeline_step<false, true>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+      __builtin_amdgcn_s_setprio(0);
+      issue_ahead(hl, t, 2);
       pipeline_step<false, true>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
     }
     // the last tile: the next head's tile 0 is outstanding behind it, unless this head is the last
