@@ -386,12 +386,13 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   // per wave each); wait for tile t, publish it, refill tile t-2's slot with tile t+2, then the two
   // pipeline steps of t (`slot` = t % kStages). Tile t+2's K goes out after the barrier and its V^T
   // between the two steps, so that the eight waves' loads reach the texture unit in two bursts
-  // rather than one that every wave waits behind. The first step runs at wave priority 1 and the
-  // second at 0: the two waves of a SIMD start the tile together and the older one, favoured by the
-  // arbiter, gets ahead; a wave still in its first step then wins over one already in its second,
-  // which keeps the pair near each other, one's exps beside the other's MFMAs, rather than the
-  // older one idling at the next barrier while the younger finishes alone. Loads and results are
-  // those of the unpartitioned tile (bit-identical).
+  // rather than one that every wave waits behind. Wave priorities: the two waves of a SIMD (w and
+  // w + 4) start the tile together and the older, favoured by the arbiter, gets ahead, then idles
+  // at the next barrier while the younger finishes alone. So the first step runs at priority 1 and
+  // the older wave drops to 0 for the second while the younger stays at 1: a wave still in its
+  // first step wins over one in its second, and the younger wins their second steps, which keeps
+  // the pair together, one's exps beside the other's MFMAs. Loads and results are those of the
+  // unpartitioned tile (bit-identical).
   auto steady_tile = [&](int t, int slot) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerTile));
     __syncthreads();
@@ -399,9 +400,10 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     const int prev = (slot + kStages - 1) % kStages;
     __builtin_amdgcn_s_setprio(1);
     pipeline_step<false, kShortKV>(sK[slot], 0, sV[prev], 1, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
-    __builtin_amdgcn_s_setprio(0);
+    if (wave < 4) __builtin_amdgcn_s_setprio(0);
     if (t + 2 < ntiles) issue_tile_v(t + 2);
     pipeline_step<false, kShortKV>(sK[slot], 1, sV[slot], 0, qf, negc, s_prev, acc_o, lsum, col, hq, 32);
+    __builtin_amdgcn_s_setprio(0);
   };
   for (int t = 1; t < ntiles - 1; ++t) steady_tile(t, t % kStages);
   if (ntiles > 1) {
