@@ -299,8 +299,17 @@ constexpr int kStageWave = 16384;  // LDS staging bytes per wave
 // Buffer resource over `rows` rows of `row_bytes` bytes from p (rows clamped to [0, 64] by the
 // caller): the hardware drops stores past the extent and returns zero for loads past it. Offsets stay
 // below 64 rows x row_bytes < 2^31 (ldo < 2^22, checked on the host).
+// Every input is the same in all lanes (tile, wave and half indices), but the compiler did not prove
+// it and wrapped each store through the resource in a loop over distinct resource values
+// (readfirstlane, 64-bit compares, exec masking: about a dozen instructions per store); taking the
+// address and extent through readfirstlane keeps the resource in scalar registers.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, int rows, uint32_t row_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)((uint32_t)rows * row_bytes), 0x00020000);
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint32_t n = __builtin_amdgcn_readfirstlane((uint32_t)rows * row_bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)n,
+                                           0x00020000);
 }
 // 16-byte store through such a resource, non-temporal (cache policy 2): the tile is written once
 // and read by the next kernel long after it would have left L2, and streaming it past L2 keeps the
