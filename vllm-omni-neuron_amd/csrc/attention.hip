@@ -456,21 +456,23 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
     uint32_t sw = 0;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      float y[16];
-      int e = 0;
+      // bf16 pairs; the block's largest exponent field is that of the largest (bits & 0x7fff)
+      uint32_t pp[8];
+      u16x2_t mag = {0, 0};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        y[r] = round_bf16(acc_o[dt][r] * inv);
-        e = max(e, exp_field(y[r]));
+      for (int r = 0; r < 16; r += 2) {
+        pp[r / 2] = pack_bf16x2(acc_o[dt][r] * inv, acc_o[dt][r + 1] * inv);
+        mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2_t, pp[r / 2] & 0x7FFF7FFFu));
       }
+      int e = (int)(max(mag[0], mag[1]) >> 7);
       e = max_with_lane_xor32(e);
       const int sx = max(e - 7, 0);
-      const float f = mx_inv_scale(sx);
+      const float sc = __uint_as_float((uint32_t)sx << 23);
       sw |= (uint32_t)sx << (8 * dt);
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
         const int d = dt * 32 + gi * 8 + hq * 4;
-        const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+        const uint32_t c4 = cvt_e4m3x4_scaled(pp[2 * gi], pp[2 * gi + 1], sc);
         *reinterpret_cast<uint32_t*>(stg + col * 128 + ((((d >> 4) ^ (col & 7)) << 4) | (d & 15))) = c4;
       }
     }
@@ -735,21 +737,23 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
       uint32_t sw = 0;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        float y[16];
-        int e = 0;
+        // bf16 pairs; the block's largest exponent field is that of the largest (bits & 0x7fff)
+        uint32_t pp[8];
+        u16x2_t mag = {0, 0};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          y[r] = round_bf16(acc_o[dt][r] * inv);
-          e = max(e, exp_field(y[r]));
+        for (int r = 0; r < 16; r += 2) {
+          pp[r / 2] = pack_bf16x2(acc_o[dt][r] * inv, acc_o[dt][r + 1] * inv);
+          mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2_t, pp[r / 2] & 0x7FFF7FFFu));
         }
+        int e = (int)(max(mag[0], mag[1]) >> 7);
         e = max_with_lane_xor32(e);
         const int sx = max(e - 7, 0);
-        const float f = mx_inv_scale(sx);
+        const float sc = __uint_as_float((uint32_t)sx << 23);
         sw |= (uint32_t)sx << (8 * dt);
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int d = dt * 32 + gi * 8 + hq * 4;
-          const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+          const uint32_t c4 = cvt_e4m3x4_scaled(pp[2 * gi], pp[2 * gi + 1], sc);
           *reinterpret_cast<uint32_t*>(stg + col * 128 + ((((d >> 4) ^ (col & 7)) << 4) | (d & 15))) = c4;
         }
       }

@@ -407,25 +407,25 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
         epi_values<kScaled>(acc[i][j], ev, i, kScaled ? vec[768 + wm * 128 + j * 32 + r32] : 1.0f, v);
         if constexpr (EPI == WANMI_EPI_GELU_MX) {
           // GELU rounded to bf16 two values per conversion; the block's largest exponent field is
-          // that of its largest |y|, taken as the largest (bits & 0x7fff) of the packed bf16 pairs
-          float y[16];
+          // that of its largest |y|, taken as the largest (bits & 0x7fff) of the packed bf16 pairs;
+          // the codes come from the packed pairs by the scaled conversion
+          uint32_t pp[8];
           u16x2 mag = {0, 0};
 #pragma unroll
           for (int q = 0; q < 16; q += 2) {
             const uint32_t p = pack_bf16x2(gelu_tanh(v[q]), gelu_tanh(v[q + 1]));
-            y[q] = bf16_lo(p);
-            y[q + 1] = bf16_hi(p);
+            pp[q / 2] = p;
             mag = __builtin_elementwise_max(mag, __builtin_bit_cast(u16x2, p & 0x7FFF7FFFu));
           }
           int e = (int)(max(mag[0], mag[1]) >> 7);
           e = max_with_lane_xor32(e);  // lanes l and l^32 hold the two halves of the 32-block
           const int sx = max(e - 7, 0);
-          const float f = mx_inv_scale(sx);
+          const float sc = __uint_as_float((uint32_t)sx << 23);
           sbytes |= (uint32_t)sx << (8 * i);
 #pragma unroll
           for (int gi = 0; gi < 4; ++gi) {
             // features 32 i + 8 gi + 4 h .. +3: chunk 2 i + (gi >> 1), byte 8 (gi & 1) + 4 h
-            const uint32_t c4 = cvt_e4m3x4(y[gi * 4] * f, y[gi * 4 + 1] * f, y[gi * 4 + 2] * f, y[gi * 4 + 3] * f);
+            const uint32_t c4 = cvt_e4m3x4_scaled(pp[2 * gi], pp[2 * gi + 1], sc);
             *reinterpret_cast<uint32_t*>(stage + stg8(tok, 2 * i + (gi >> 1)) + 8 * (gi & 1) + 4 * h) = c4;
           }
         } else {

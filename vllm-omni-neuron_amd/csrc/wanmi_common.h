@@ -72,6 +72,19 @@ __device__ __forceinline__ uint32_t cvt_e4m3x4(float a, float b, float c, float 
   r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
   return (uint32_t)r;
 }
+// Four bf16 values, packed two per word (low half first), times 2^(127 - s) -> four e4m3fn codes in
+// one word, by the hardware's scaled conversion: `sc` carries the e8m0 exponent s in a float's
+// exponent field (s << 23; s = 0 means 2^-127). For |value x 2^(127 - s)| < 256, the MX range, the
+// codes equal cvt_e4m3x4 of the four values multiplied by mx_inv_scale(s) (checked exhaustively on
+// MI355X over every bf16 input for s = 0 .. 247).
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_e4m3x4_scaled(uint32_t p01, uint32_t p23, float sc) {
+  i16x2_t r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, p01), sc, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, p23), sc, true);
+  return __builtin_bit_cast(uint32_t, r);
+}
 
 // ------------------------------------------------------------------------------------------------
 // Device: buffer descriptors and direct-to-LDS loads
