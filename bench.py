@@ -192,6 +192,27 @@ def block_720p(pkg, w, cross, temb, dev, reps=3):
     }
 
 
+def copy_ceiling(traffic_bytes, adaln_gbs, reps=20):
+    """Device-to-device copy moving the adaLN launch's bytes (half read, half written), timed with
+    HIP events: the practical HBM rate of a streaming kernel on this box, beside the nominal 8 TB/s."""
+    n = traffic_bytes // 2
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    gbs = traffic_bytes / ms / 1e6
+    return {"bytes_per_copy": 2 * n, "ms_per_copy": round(ms, 4), "gbs": round(gbs, 1),
+            "adaln_frac_of_copy": round(adaln_gbs / gbs, 3)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -293,6 +314,7 @@ def main():
             "traffic": load_traffic(S),
         },
     }
+    result["hbm_copy_ceiling"] = copy_ceiling(plain, result["adaln_quant_gbs"])
     if not args.no_720p:
         result["p720"] = block_720p(pkg, blocks[0], crosses[0], temb, dev)
     if not args.no_cpu_baseline:
