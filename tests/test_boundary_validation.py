@@ -119,6 +119,12 @@ def test_drop_in_argument_checks(pkg, w):
         pkg.row_mx_mlp(packed, w, w, up_w_scale=torch.ones(N + 1))
     with pytest.raises(ValueError, match="K/4, N, 4"):
         pkg.packed_weight_to_mx(torch.zeros(K, N, dtype=torch.uint8).view(torch.float8_e4m3fn))
+    with pytest.raises(ValueError, match="bf16"):
+        pkg.row_quantize_packed(torch.zeros(M, K))
+    with pytest.raises(ValueError, match=r"\[T, H\]"):
+        pkg.row_quantize_packed(torch.zeros(K, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError):  # no CPU fallback
+        pkg.row_quantize_packed(torch.zeros(M, K, dtype=torch.bfloat16))
 
 
 def test_packed_reference_weight_layout(pkg):

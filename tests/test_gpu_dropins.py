@@ -161,6 +161,56 @@ def test_cross_query_projection_nbsd(pkg, dev, qkv_case):
     _close(out.cpu(), ref, "cross Q")
 
 
+@pytest.mark.parametrize("shape", [(512, 5120), (2, 37, 96), (0, 64)])
+def test_row_quantize_packed(pkg, dev, shape):
+    """The context row-pack (row_mx_kernels.py:12-45) bit for bit against the oracle's ROW rule,
+    2-D and batched, with a zero row (dequant scale floored at 1e-6) and rows of very different
+    magnitudes."""
+    g = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn(*shape, generator=g)
+    if x.numel():
+        flat = x.view(-1, shape[-1])
+        flat[0] = 0.0
+        flat[-1] *= 3.0e4
+        if flat.shape[0] > 2:
+            flat[1] *= 1.0e-5
+    x = x.to(torch.bfloat16)
+    out = pkg.row_quantize_packed(x.to(dev))
+    assert out.dtype == torch.float8_e4m3fn and out.shape == (*shape[:-1], shape[-1] + 4)
+    codes, dq = omx.row_quantize(x.float().numpy())
+    np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), omx.row_pack(codes, dq))
+
+
+def test_row_packed_context_cross_kv(pkg, dev, qkv_case):
+    """``WanCrossAttentionFP8.project_kv`` on the row-packed context (row_mx_modules.py:509-542,
+    wan2_2_transformer.py:1686-1696): K with the across-heads norm and V, both NBSd, from one packed
+    input, against the fp64 ROW_MX projections of the oracle's packing."""
+    c = qkv_case
+    dim, nh = c["dim"], c["nh"]
+    ct = pkg.common_types
+    g = torch.Generator().manual_seed(5)
+    ctx = torch.randn(1, 96, dim, generator=g).to(torch.bfloat16)
+    packed = pkg.row_quantize_packed(ctx.to(dev))
+    codes, dq = omx.row_quantize(ctx.float().numpy())
+    np.testing.assert_array_equal(packed.view(torch.uint8).cpu().numpy(), omx.row_pack(codes, dq))
+    wk, wv = c["w_nat"][:, dim : 2 * dim], c["w_nat"][:, 2 * dim :]
+    sk, sv = c["scales"][dim : 2 * dim], c["scales"][2 * dim :]
+    bk, bv = c["bias"][dim : 2 * dim], c["bias"][2 * dim :]
+    key = pkg.row_mx_qkv_proj(
+        packed, _pack(wk).to(dev), sk.to(dev)[None], bk.to(dev)[None], num_heads=nh, head_dim=HD,
+        qk_norm_pre_rope=ct.QKNormConfig(ct.NormType.RMS_NORM_ACROSS_HEADS, None, 1e-6),
+        qk_norm_pre_rope_q_gamma=c["gk"].to(dev)[None], norm_eps=1e-6, output_layout=ct.QKVOutputLayout.NBSd,
+    )
+    value = pkg.row_mx_qkv_proj(packed, _pack(wv).to(dev), sv.to(dev)[None], bv.to(dev)[None], num_heads=nh,
+                                head_dim=HD, output_layout=ct.QKVOutputLayout.NBSd)
+    assert key.shape == value.shape == (nh, 1, 96, HD)
+    lin_k = _row_mx_oracle(packed, wk, sk.numpy(), bk.numpy()).float().to(torch.bfloat16).view(1, 96, dim)
+    lin_v = _row_mx_oracle(packed, wv, sv.numpy(), bv.numpy()).float().to(torch.bfloat16).view(1, 96, dim)
+    ref_k = orope.rms_norm_across_heads(lin_k, c["gk"]).view(1, 96, nh, HD).permute(2, 0, 1, 3)
+    _close(key.cpu(), ref_k, "cross K")
+    _close(value.cpu(), lin_v.view(1, 96, nh, HD).permute(2, 0, 1, 3), "cross V")
+
+
 def test_row_mx_mlp(pkg, dev):
     B, S, dim, ffn = 2, 200, 1024, 2816
     g = torch.Generator().manual_seed(12)

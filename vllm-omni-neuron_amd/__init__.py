@@ -1,7 +1,7 @@
 """MI355X (gfx950) implementation of the Wan2.2-A14B DiT-block hot path.
 
 Drop-ins for the reecedantin/vllm-omni-neuron op boundary of the Wan2.2 transformer block
-(``adaln_modulate``, ``row_mx_qkv_proj``, ``row_mx_mlp``, ``row_mx_o_proj``,
+(``adaln_modulate``, ``row_quantize_packed``, ``row_mx_qkv_proj``, ``row_mx_mlp``, ``row_mx_o_proj``,
 ``wan_cp_self_attention``/``_nki_attend``, ``ring_attention_const_max_fwd``), each backed by
 hand-written HIP kernels in ``libwanmi.so`` and called through its C ABI (``include/wanmi.h``).
 
@@ -19,6 +19,7 @@ from .row_mx_kernels import (  # noqa: F401
     packed_weight_to_mx,
     quantize_weight_mx,
     row_mx_mlp,
+    row_quantize_packed,
 )
 from . import rope  # noqa: F401
 from .rope import WanRotaryPosEmbed, rope_tables  # noqa: F401

@@ -3,6 +3,7 @@
 Drop-ins for the reference's ROW_MX projection launchers
 (vllm_omni_neuron/diffusion/quantization/row_mx_kernels.py):
 
+- :func:`row_quantize_packed` (row_mx_kernels.py:12-45): bf16 rows to the packed ROW layout.
 - :func:`row_mx_mlp` (row_mx_kernels.py:141-198): gate-less GELU-tanh MLP, up projection with the
   GELU + MX re-quantization fused in its epilogue, then the down projection.
 - :func:`row_mx_qkv_proj` (row_mx_kernels.py:48-111) and :func:`row_mx_o_proj` (114-138) are in
@@ -272,6 +273,28 @@ def mxfp8_qkv_linear(x, weight: MXWeight, *, vt_col0: int, row_sumsq: torch.Tens
     )
     _lib.check(status, "wanmi_mxfp8_gemm_qkv")
     return qk.reshape(*lead, vt_col0), vt
+
+
+def row_quantize_packed(hidden: torch.Tensor) -> torch.Tensor:
+    """bf16 rows ``[T, H]`` or ``[B, T, H]`` -> ROW-packed ``[..., H + 4]`` float8_e4m3fn bytes: each
+    row's e4m3 codes, then the 4 little-endian bytes of its fp32 dequant scale
+    ``max(amax / 448, 1e-6)`` (codes = RNE(y / scale)), the layout the ROW_MX projections read.
+
+    Drop-in for the reference's ``row_quantize_packed`` (row_mx_kernels.py:12-45: nkilib's
+    rmsnorm_quant with NO_NORM, ROW quantization, no clip bound), which the model runs once per
+    generation on the text context before every block's cross-attention K/V projection
+    (wan2_2_transformer.py:1686-1691, row_mx_modules.py:509-542). Here it is one launch of the fused
+    adaLN kernel in its NO_NORM / ROW mode, whose rule is the ROW branch of adaln_quant_torch.py:
+    131-142 (the vendored ROW path that mirrors rmsnorm_quant, adaln_quant.py:472-530). H must be a
+    multiple of 32 (at most 16384).
+    """
+    if hidden.dim() not in (2, 3):
+        raise ValueError(f"row_quantize_packed expects [T, H] or [B, T, H], got {tuple(hidden.shape)}")
+    if hidden.dtype != torch.bfloat16:
+        raise ValueError(f"row_quantize_packed expects bf16 rows, got {hidden.dtype}")
+    H = hidden.shape[-1]
+    packed = adaln_quant_2d(hidden.reshape(-1, H), None, None, eps=1e-6, norm_type="none", quant="row")
+    return packed.view(*hidden.shape[:-1], H + 4)
 
 
 def row_mx_mlp(
