@@ -137,3 +137,23 @@ def test_packed_reference_weight_layout(pkg):
         assert int(codes[n, k]) == int(phys[k // 4, n, k % 4])
     assert mw.rope_pairs == "halves" and bool((mw.scales == 127).all())
     assert mw.col_scale.shape == (Nn,) and float(mw.col_scale[7]) == 0.5
+
+
+def test_registered_attention_op(pkg):
+    """``wan_transformer::attention_cte`` is registered as a functional torch op (the reference's
+    ``nki_op`` registration), propagates shapes without running ([BN, S_q, D] -> [BN, D, S_q]) and
+    refuses CPU tensors (no CPU fallback)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    op = torch.ops.wan_transformer.attention_cte
+    with FakeTensorMode():
+        q = torch.empty(6, 300, 128, dtype=torch.bfloat16)
+        k = torch.empty(6, 77, 128, dtype=torch.bfloat16)
+        o = op(q, k, k)
+        assert o.shape == (6, 128, 300) and o.dtype == torch.bfloat16
+    with pytest.raises(RuntimeError):
+        op(torch.zeros(2, 8, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 128, dtype=torch.bfloat16),
+           torch.zeros(2, 8, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="BN, S, 128"):
+        pkg.attention_ops.attention_cte(torch.zeros(2, 8, 128), torch.zeros(3, 8, 128), torch.zeros(3, 8, 128))
+    assert pkg.attention_ops.register_torch_ops() is False  # registered once per process

@@ -247,5 +247,14 @@ def test_dropins_match_reference_layouts(pkg, dev):
     _check_attn(o2.transpose(2, 3), ref)
     o3 = ops.ring_attention_const_max_fwd(q.to(dev), k.to(dev), v.to(dev), softmax_scale=s).cpu()  # [B,N,S,D]
     _check_attn(o3, ref)
+    # the registered op as _nki_attend launches it (wan2_2_transformer.py:668-674): [BN, S, D] with
+    # q pre-scaled, d-major [BN, D, S] out; 77 keys (a ragged last tile)
+    qb, kb, vb = (t.transpose(1, 2).reshape(B * N, -1, D) for t in (q, k[:, :77], v[:, :77]))
+    ref4 = oa.torch_attend(qb[None], kb[None], vb[None], s, dtype=torch.float64)[0]  # [BN, S, D]
+    o4 = torch.ops.wan_transformer.attention_cte((qb.float() * s).to(torch.bfloat16).to(dev), kb.to(dev), vb.to(dev))
+    assert o4.shape == (B * N, D, S)
+    ref4s = oa.torch_attend(((qb.float() * s).to(torch.bfloat16))[None], kb[None], vb[None], 1.0, dtype=torch.float64)[0]
+    _check_attn(o4.cpu().transpose(1, 2), ref4s)
+    _check_attn(o4.cpu().transpose(1, 2), ref4)
     with pytest.raises(NotImplementedError):
         ops.wan_cp_self_attention(q.to(dev), k.to(dev), v.to(dev), s, 2, None, None)

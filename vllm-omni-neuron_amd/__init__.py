@@ -31,5 +31,6 @@ from .attention_ops import (  # noqa: F401
     row_mx_qkv_proj,
     wan_cp_self_attention,
 )
+attention_ops.register_torch_ops()
 from . import block  # noqa: F401
 from . import comfy_fp8_checkpoint  # noqa: F401

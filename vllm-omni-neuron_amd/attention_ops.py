@@ -223,6 +223,33 @@ def _nki_attend(query, key, value, scale):
     return torch.stack(outs, dim=0) if len(outs) > 1 else outs[0].unsqueeze(0)
 
 
+def attention_cte(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """The reference's registered attention op ``wan_transformer::attention_cte``
+    (wan2_2_transformer.py:165-171, launching ``_wan_attention_kernel`` 83-108): ``[BN, S_q, 128]``
+    q already multiplied by the softmax scale, ``[BN, S_k, 128]`` k and v, non-causal, unit scale,
+    d-major ``[BN, 128, S_q]`` out. Each of the BN rows is one head of the constant-max kernel."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or q.shape[0] != k.shape[0] or k.shape != v.shape:
+        raise ValueError(f"attention_cte expects [BN, S, 128] q/k/v, got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    return _attend_bsnd(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), 1.0, OUT_DMAJOR)
+
+
+def register_torch_ops() -> bool:
+    """Registers :func:`attention_cte` as the functional torch op ``wan_transformer::attention_cte``
+    (``mutates_args=()``, as the reference's ``nki_op`` registration, lite_compat.py:88-95), with a
+    fake implementation for shape propagation. Returns False, registering nothing, when an op of
+    that name already exists in the process."""
+    if hasattr(torch.ops, "wan_transformer") and hasattr(torch.ops.wan_transformer, "attention_cte"):
+        return False
+    op = torch.library.custom_op("wan_transformer::attention_cte", attention_cte, mutates_args=())
+
+    @op.register_fake
+    def _(q, k, v):
+        return q.new_empty((q.shape[0], q.shape[2], q.shape[1]))
+
+    return True
+
+
 def ring_attention_const_max_fwd(q, k, v, replica_groups=None, num_workers=1, softmax_scale=None,
                                  training=False, lse_dtype=None, kv_prefetch_depth=2):
     """Token-major ``[b, S, h, d]`` q/k/v -> ``[b, h, S, d]`` with the constant-max softmax.
