@@ -157,3 +157,37 @@ def test_registered_attention_op(pkg):
     with pytest.raises(ValueError, match="BN, S, 128"):
         pkg.attention_ops.attention_cte(torch.zeros(2, 8, 128), torch.zeros(3, 8, 128), torch.zeros(3, 8, 128))
     assert pkg.attention_ops.register_torch_ops() is False  # registered once per process
+
+
+def test_adaln_quant_kernel_argument_checks(pkg):
+    """The kernel-level adaLN drop-in keeps the reference's checks (adaln_quant.py:70-114, 242-290)
+    and refuses what gfx950 does not produce, all before any launch."""
+    A, NT, QT, DM = pkg.AdaLNQuantKernelArgs, pkg.NormType, pkg.QuantizationType, pkg.DtypeMode
+    with pytest.raises(ValueError, match="normalization"):
+        A(norm_type=NT.RMS_NORM_ACROSS_HEADS)
+    with pytest.raises(ValueError, match="quantization"):
+        A(quantization_type=QT.ROW_MX)
+    with pytest.raises(ValueError, match="Lower bound"):
+        A(lower_bound=-1.0)
+    with pytest.raises(ValueError, match="Epsilon"):
+        A(eps=-1e-6)
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    k = pkg.adaln_quant_kernel
+    with pytest.raises(NotImplementedError, match="MX"):
+        k(x, A(quantization_type=QT.MX), dtype_mode=DM.OCP)
+    with pytest.raises(NotImplementedError, match="NON_OCP"):
+        k(x, A(quantization_type=QT.ROW))  # the reference's default dtype mode
+    with pytest.raises(NotImplementedError, match="clip bound"):
+        k(x, A(quantization_type=QT.ROW, lower_bound=8.0), dtype_mode=DM.OCP)
+    with pytest.raises(ValueError, match="Rank of hidden"):
+        k(torch.zeros(64, dtype=torch.bfloat16), A())
+    with pytest.raises(ValueError, match="gate requires residual"):
+        k(x, A(), gate=torch.ones(64))
+    with pytest.raises(ValueError, match="vector length"):
+        k(x, A(), mul=torch.ones(32))
+    with pytest.raises(ValueError, match="first dimension"):
+        k(x, A(), add=torch.ones(2, 64))
+    with pytest.raises(ValueError, match="residual"):
+        k(x, A(), residual=torch.zeros(4, 32, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError):  # no CPU fallback
+        k(x, A(quantization_type=QT.ROW), dtype_mode=DM.OCP)

@@ -129,3 +129,40 @@ def test_e4m3_conversion_kat_every_bf16(pkg, dev):
     dst = torch.empty(v.size, dtype=torch.uint8, device=dev)
     pkg._lib.check(lib.wanmi_e4m3_encode(pkg._lib.ptr(src), pkg._lib.ptr(dst), v.size, pkg._lib.stream_of(src)), "e4m3")
     np.testing.assert_array_equal(dst.cpu().numpy(), fp8.e4m3_encode(v))
+
+
+@pytest.mark.parametrize("case", ["layer_row", "rms_none_3d", "none_row_residual", "layer_none_residual_nogate"])
+def test_adaln_quant_kernel_dropin(pkg, dev, case):
+    """The kernel-level drop-in as the bridge launches it (adaln_kernels.py:150-201): bf16 ``[1, H]``
+    mul / add, fp32 gate, OCP ROW output, a rank-3 hidden; bit-exact against the oracle."""
+    A, NT, QT, DM = pkg.AdaLNQuantKernelArgs, pkg.NormType, pkg.QuantizationType, pkg.DtypeMode
+    norm, quant, resid, shape = {
+        "layer_row": (NT.LAYER_NORM, QT.ROW, False, (300, 5120)),
+        "rms_none_3d": (NT.RMS_NORM, QT.NONE, False, (2, 37, 512)),
+        "none_row_residual": (NT.NO_NORM, QT.ROW, True, (64, 1024)),
+        "layer_none_residual_nogate": (NT.LAYER_NORM, QT.NONE, "nogate", (33, 544)),
+    }[case]
+    H = shape[-1]
+    g = torch.Generator().manual_seed(H + len(shape))
+    x = torch.randn(*shape, generator=g).to(torch.bfloat16)
+    mul = (1 + 0.5 * torch.randn(1, H, generator=g)).to(torch.bfloat16)
+    add = (0.5 * torch.randn(1, H, generator=g)).to(torch.bfloat16)
+    res = torch.randn(*shape, generator=g).to(torch.bfloat16) if resid else None
+    gate = torch.randn(1, H, generator=g) if resid is True else None
+    args = A(norm_type=norm, quantization_type=quant, eps=1e-6)
+    out = pkg.adaln_quant_kernel(x.to(dev), args, mul.to(dev), add.to(dev), DM.OCP,
+                                 None if res is None else res.to(dev), None if gate is None else gate.to(dev))
+    ref = oracle_adaln.adaln_quant(_np(x).reshape(-1, H), mul.float().numpy().reshape(H), add.float().numpy().reshape(H),
+                                   eps=1e-6, norm_type=norm.value, quant=quant.value,
+                                   residual=None if res is None else _np(res).reshape(-1, H),
+                                   gate=None if gate is None else gate.numpy().reshape(H))
+    if res is not None:
+        res_out, out = out
+        assert res_out.shape == shape
+        np.testing.assert_array_equal(res_out.float().cpu().numpy().reshape(-1, H), ref["residual_out"])
+    if quant == QT.ROW:
+        assert out.shape == (*shape[:-1], H + 4) and out.dtype == torch.float8_e4m3fn
+        np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy().reshape(-1, H + 4), ref["packed"])
+    else:
+        assert out.shape == shape and out.dtype == torch.bfloat16
+        np.testing.assert_array_equal(out.float().cpu().numpy().reshape(-1, H), ref["y"])

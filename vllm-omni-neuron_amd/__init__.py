@@ -10,8 +10,8 @@ The directory name contains dashes, so it is imported under the module name
 """
 
 from . import _lib  # noqa: F401
-from .adaln_kernels import adaln_modulate  # noqa: F401
-from .common_types import MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401
+from .adaln_kernels import AdaLNQuantKernelArgs, adaln_modulate, adaln_quant_kernel  # noqa: F401
+from .common_types import DtypeMode, MXTensor, NormType, QKNormConfig, QKVOutputLayout, QuantizationType  # noqa: F401
 from .row_mx_kernels import (  # noqa: F401
     MXWeight,
     mxfp8_linear,

@@ -16,10 +16,12 @@ Differences, all deliberate:
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import _lib
-from .common_types import MXTensor
+from .common_types import DtypeMode, MXTensor, NormType, QuantizationType
 
 _MAX_HIDDEN = 16384
 _SUPPORTED_NORMS = ("layer_norm", "rms_norm", "none")
@@ -177,3 +179,101 @@ def adaln_modulate(
     if hidden.dim() == 2:
         residual_out = residual_out[0]
     return residual_out, out
+
+
+@dataclass(frozen=True)
+class AdaLNQuantKernelArgs:
+    """Configuration of :func:`adaln_quant_kernel` (the reference's dataclass of the same name,
+    adaln_quant.py:70-114, with the same fields, defaults and checks)."""
+
+    norm_type: NormType = NormType.LAYER_NORM
+    quantization_type: QuantizationType = QuantizationType.NONE
+    eps: float = 1e-6
+    lower_bound: float = 0.0
+
+    def __post_init__(self):
+        if self.norm_type not in (NormType.LAYER_NORM, NormType.RMS_NORM, NormType.NO_NORM):
+            raise ValueError(f"{self.norm_type.name} normalization is not supported")
+        if self.quantization_type not in (QuantizationType.NONE, QuantizationType.ROW, QuantizationType.MX):
+            raise ValueError(f"{self.quantization_type.name} quantization is not supported")
+        if not self.lower_bound >= 0:
+            raise ValueError(f"Lower bound must be non-negative but got {self.lower_bound}")
+        if not self.eps >= 0:
+            raise ValueError(f"Epsilon must be non-negative but got {self.eps}")
+
+    def has_lower_bound(self) -> bool:
+        return self.lower_bound is not None and self.lower_bound > 0.000001
+
+
+def _vector(vec: torch.Tensor | None, name: str, H: int) -> torch.Tensor | None:
+    """A per-hidden vector ``[H]`` or ``[1, H]`` (any float dtype) -> contiguous fp32 ``[H]``."""
+    if vec is None:
+        return None
+    if vec.dim() not in (1, 2):
+        raise ValueError(f"Rank of {name} must be 1 or 2 but got {vec.dim()}")
+    if vec.shape[-1] != H:
+        raise ValueError(f"{name} vector length must equal {H} but got {vec.shape[-1]}")
+    if vec.dim() == 2 and vec.shape[0] > 1:
+        raise ValueError(f"{name} first dimension {vec.shape[0]} must be at most 1")
+    return vec.reshape(H).to(torch.float32).contiguous()
+
+
+def adaln_quant_kernel(
+    hidden: torch.Tensor,
+    kargs: AdaLNQuantKernelArgs,
+    mul: torch.Tensor | None = None,
+    add: torch.Tensor | None = None,
+    dtype_mode: DtypeMode = DtypeMode.NON_OCP,
+    residual: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+):
+    """Kernel-level drop-in for ``adaln_quant_kernel`` (vllm_omni_neuron/kernels/nkilib/experimental/
+    norm/adaln_quant.py:117-234), as ``adaln_modulate`` launches it per batch element
+    (adaln_kernels.py:150-201): ``[..., H]`` bf16 ``hidden`` (rank >= 2, all leading dims are rows),
+    ``mul`` / ``add`` / ``gate`` ``[H]`` or ``[1, H]``. Returns the modulated ``[..., H]`` bf16, or
+    ``[..., H + 4]`` float8_e4m3fn for ROW (codes, then the row's fp32 dequant scale); with
+    ``residual``, ``(residual_out, modulated)`` where ``residual_out = bf16(residual + gate *
+    hidden)``. One launch of the fused kernel.
+
+    As in the reference, MX quantization is not produced here (the caller's MX path is
+    ``adaln_modulate(quant="mx")``) and ``gate`` requires ``residual``. gfx950 FP8 is the OCP e4m3fn
+    format, so ROW output needs ``dtype_mode`` OCP or AUTO (the reference's default NON_OCP is its
+    e4m3 with max 240), and the ROW clip bound (``lower_bound`` > 0) is not implemented: both raise
+    NotImplementedError. mul / add are consumed as given (the reference's bridge rounds them to the
+    hidden dtype before this call).
+    """
+    if not isinstance(kargs, AdaLNQuantKernelArgs):
+        raise TypeError("kargs must be an AdaLNQuantKernelArgs")
+    if kargs.quantization_type == QuantizationType.MX:
+        raise NotImplementedError("MX quantization is not implemented in adaln_quant_kernel; the caller must use "
+                                  "adaln_modulate(quant='mx').")
+    row = kargs.quantization_type == QuantizationType.ROW
+    if row and dtype_mode == DtypeMode.NON_OCP:
+        raise NotImplementedError("NON_OCP e4m3 (max 240) is not an FP8 format of gfx950; use DtypeMode.OCP")
+    if row and kargs.has_lower_bound():
+        raise NotImplementedError("the ROW clip bound (lower_bound > 0) is not implemented")
+    if hidden.dim() < 2:
+        raise ValueError(f"Rank of hidden must be at least 2 but got {hidden.dim()}")
+    if hidden.dtype != torch.bfloat16:
+        raise ValueError(f"hidden must be bfloat16, got {hidden.dtype}")
+    H = hidden.shape[-1]
+    if H > _MAX_HIDDEN or H % 32:
+        raise ValueError(f"hidden size {H} must be a multiple of 32 and <= {_MAX_HIDDEN}")
+    if gate is not None and residual is None:
+        raise ValueError("gate requires residual (gate scales the sub-layer output before the residual add)")
+    if residual is not None and (residual.shape != hidden.shape or residual.dtype != torch.bfloat16):
+        raise ValueError(f"residual must be bf16 {tuple(hidden.shape)}, got {residual.dtype} {tuple(residual.shape)}")
+    res = adaln_quant_2d(
+        hidden.reshape(-1, H),
+        _vector(mul, "mul", H),
+        _vector(add, "add", H),
+        eps=kargs.eps,
+        norm_type=kargs.norm_type.value,
+        quant="row" if row else "none",
+        residual=None if residual is None else residual.reshape(-1, H),
+        gate=_vector(gate, "gate", H),
+    )
+    lead = hidden.shape[:-1]
+    if residual is None:
+        return res.view(*lead, res.shape[-1])
+    return res[0].view(*lead, H), res[1].view(*lead, res[1].shape[-1])

@@ -1,7 +1,7 @@
 """Boundary vocabulary shared by the ops: the reference's enums plus the MX tensor pair.
 
 The enum members mirror vllm_omni_neuron/kernels/nkilib/core/utils/common_types.py (NormType,
-QuantizationType, QKVOutputLayout) so call sites read the same; only the members the Wan DiT
+QuantizationType, DtypeMode, QKVOutputLayout) so call sites read the same; only the members the Wan DiT
 path uses are kept.
 """
 
@@ -25,6 +25,15 @@ class QuantizationType(enum.Enum):
     ROW = "row"
     MX = "mx"
     ROW_MX = "row_mx"
+
+
+class DtypeMode(enum.Enum):
+    """FP8 e4m3 variant of a ROW-quantized output: NON_OCP (max 240), OCP (e4m3fn, max 448), AUTO
+    (what the hardware supports: OCP on gfx950)."""
+
+    NON_OCP = "non_ocp"
+    OCP = "ocp"
+    AUTO = "auto"
 
 
 class QKVOutputLayout(enum.Enum):
