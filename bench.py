@@ -3,7 +3,9 @@
 Workload: 40 Wan2.2-A14B blocks (dim 5120, 40 heads x 128, FFN 13824), S = 32760 tokens
 (21x30x52 latent grid, 480x832x81 frames), 512 text tokens, MXFP8 projections and bf16 constant-max
 attention, one CFG branch, cross-attention K/V cached (projected once before timing, as the
-reference does per generation). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
+reference does per generation), the RoPE tables built inside every timed forward (as the reference
+builds them per forward). After the metric the same 40-block forward is measured at 720p
+(21x45x80 = 75600 tokens). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
 seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic data.
 
 Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). Per-kernel times
@@ -40,7 +42,7 @@ def parse():
     p.add_argument("--grid", type=str, default="21,30,52", help="latent patch grid F,H,W")
     p.add_argument("--blocks", type=int, default=40)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-720p", action="store_true", help="skip the 720p (21x45x80) single-block timing")
+    p.add_argument("--no-720p", action="store_true", help="skip the 720p (21x45x80) 40-block step timing")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="also run one 256 MiB device copy, the known-size reference for HBM counters")
     return p.parse_args()
@@ -155,40 +157,39 @@ def cpu_baseline(S_full, blocks):
     }
 
 
-def block_720p(pkg, w, cross, temb, dev, reps=3):
-    """One block at the 720p step's length (21x45x80 = 75600 tokens; block 0's weights and text K/V),
-    timed after the main metric: mean of `reps` launches after one warm-up, per-kernel HIP events
-    from one more; the 40-block step is estimated as 40 x the block."""
+def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
+    """The 40-block forward at the 720p step's length (21x45x80 = 75600 tokens, 512 text tokens, the
+    same weights and cached text K/V), measured after the main metric: `warmup` untimed forwards,
+    then `steps` timed ones bracketed by device synchronizations, with per-kernel HIP events."""
     blk = pkg.block
     grid = (21, 45, 80)
     S7 = grid[0] * grid[1] * grid[2]
     gen = torch.Generator(device=dev).manual_seed(720)
     h = torch.randn(S7, DIM, device=dev, generator=gen).to(torch.bfloat16)
-    rope = pkg.rope_tables(grid, device=dev)
-    mod = blk.modulation(w.scale_shift_table[None], temb)[0]
-    blk.block_forward(w, h, temb, rope, cross, mod=mod)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        out = blk.block_forward(w, h, temb, rope, cross, mod=mod)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    for _ in range(warmup):
+        blk.dit_forward(blocks, h, temb, grid, crosses, tables=tables)
     timer = KernelTimer()
     timer.active = True
-    blk.block_forward(w, h, temb, rope, cross, mod=mod, timer=timer)
     torch.cuda.synchronize()
-    comp = {k: round(sum(v), 3) for k, v in sorted(timer.summary().items())}
-    attn_ms = comp["self_attention"]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = blk.dit_forward(blocks, h, temb, grid, crosses, timer=timer, tables=tables)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
     if not torch.isfinite(out.float()).all():
-        raise RuntimeError("non-finite 720p block output")
+        raise RuntimeError("non-finite 720p DiT output")
+    times = timer.summary()
+    comp = {k: round(sum(v) / steps, 2) for k, v in sorted(times.items())}
+    attn = times["self_attention"]
+    attn_ms = sum(attn) / len(attn)
+    n_blk = steps * len(blocks)
+    gemm_ms = sum(sum(v) for k, v in times.items() if k.startswith("gemm_")) / n_blk
     return {
-        "workload": "one Wan2.2-A14B block at 720p: 21x45x80 = 75600 tokens, 512 text tokens",
-        "seq_len": S7, "ms_per_block": round(ms, 2), "ms_per_step_estimate_40_blocks": round(40 * ms, 1),
+        "workload": f"Wan2.2-A14B DiT forward at 720p: {len(blocks)} blocks, 21x45x80 = 75600 tokens, 512 text tokens",
+        "seq_len": S7, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 1),
         "self_attention_tflops": round(4.0 * S7 * S7 * HEAD_DIM * HEADS / attn_ms / 1e9, 1),
-        "gemm_tflops": round(gemm_flops(S7) / sum(v for k, v in comp.items() if k.startswith("gemm_")) / 1e9, 1),
-        "components_ms": comp,
+        "gemm_tflops": round(gemm_flops(S7) / gemm_ms / 1e9, 1),
+        "components_ms_per_step": comp,
     }
 
 
@@ -231,7 +232,6 @@ def main():
     h0 = torch.randn(S, DIM, device=dev, generator=gen).to(torch.bfloat16)
     temb = torch.randn(6, DIM, device=dev, generator=gen)
     ctx = torch.randn(TXT, DIM, device=dev, generator=gen).to(torch.bfloat16)
-    rope = pkg.rope_tables(grid, device=dev)  # built once per generation (not timed)
     crosses = [blk.project_cross_kv(w, ctx) for w in blocks]
     tables = torch.stack([w.scale_shift_table for w in blocks])
     torch.cuda.synchronize()
@@ -245,14 +245,14 @@ def main():
 
     timer = KernelTimer()
     for _ in range(args.warmup):
-        blk.dit_forward(blocks, h0, temb, rope, crosses, tables=tables)
+        blk.dit_forward(blocks, h0, temb, grid, crosses, tables=tables)
     torch.cuda.synchronize()
 
     timer.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out = blk.dit_forward(blocks, h0, temb, rope, crosses, timer=timer, tables=tables)
+        out = blk.dit_forward(blocks, h0, temb, grid, crosses, timer=timer, tables=tables)
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1000.0
     timer.active = False
@@ -316,7 +316,7 @@ def main():
     }
     result["hbm_copy_ceiling"] = copy_ceiling(plain, result["adaln_quant_gbs"])
     if not args.no_720p:
-        result["p720"] = block_720p(pkg, blocks[0], crosses[0], temb, dev)
+        result["p720"] = step_720p(pkg, blocks, crosses, tables, temb, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(S, args.blocks)
     print(json.dumps(result), flush=True)

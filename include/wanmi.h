@@ -116,7 +116,8 @@ int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* a_scales, c
  * wanmi_mxfp8_gemm_rowsumsq writes them -- while the columns [vt_col0, N) -- V -- go to vt as V^T
  * [(N - vt_col0)/128 heads][128][vt_ld] bf16 in the key order of wanmi_transpose_heads (inside each
  * group of 16 keys: 0-3, 8-11, 4-7, 12-15), zero for tokens M .. vt_ld - 1. vt_col0 and N - vt_col0
- * are multiples of 256, vt_ld >= M, vt_ld % 64 == 0. Two launches on `stream` (Q|K, then V, whose
+ * are multiples of 256; M > 0; M <= vt_ld <= M rounded up to 256 (the V launch writes every token
+ * column of the 256-token tiles it covers, zeros past M), vt_ld % 64 == 0. Two launches on `stream` (Q|K, then V, whose
  * MFMAs take the token operand first so that four consecutive tokens of a feature are lane-local).
  * Replaces the QKV kernel of row_mx_qkv_proj (vllm_omni_neuron/diffusion/quantization/
  * row_mx_kernels.py:48-111, kernels/nkilib/core/qkv/qkv_cte.py:2725) together with the V transpose

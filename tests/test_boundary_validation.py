@@ -191,3 +191,69 @@ def test_adaln_quant_kernel_argument_checks(pkg):
         k(x, A(), residual=torch.zeros(4, 32, dtype=torch.bfloat16))
     with pytest.raises(RuntimeError):  # no CPU fallback
         k(x, A(quantization_type=QT.ROW), dtype_mode=DM.OCP)
+
+
+def _wan_mlp_kwargs(pkg, **over):
+    """The argument set the Wan FFN passes to the nkilib mlp kernel (row_mx_kernels.py:172-198)."""
+    ct = pkg.common_types
+    kw = dict(skip_gate_proj=True, activation_fn=ct.ActFnType.GELU_Tanh_Approx, normalization_type=ct.NormType.NO_NORM,
+              quantization_type=ct.QuantizationType.ROW_MX, quant_clipping_bound=None, output_dtype="bfloat16",
+              force_cte_mode=True, dtype_mode=ct.DtypeMode.AUTO,
+              gate_up_w_layout=ct.MLPGateUpWeightLayout.H_X4_INNERMOST)
+    kw.update(over)
+    return kw
+
+
+def test_kernel_mlp_rejects_other_configurations(pkg, w):
+    """The nkilib mlp signature runs only Wan's configuration; everything else is refused before
+    any tensor is touched (NotImplementedError), and a malformed weight is a ValueError."""
+    ct = pkg.common_types
+    x = torch.zeros(M, K + 4, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    bad = [
+        dict(skip_gate_proj=False),
+        dict(activation_fn=ct.ActFnType.SiLU),
+        dict(normalization_type=ct.NormType.RMS_NORM),
+        dict(quantization_type=ct.QuantizationType.MX),
+        dict(fused_add_tensor=torch.zeros(M, K, dtype=torch.bfloat16)),
+        dict(store_fused_add_result=True),
+        dict(quant_clipping_bound=240.0),
+        dict(up_clamp_upper_limit=7.0),
+        dict(store_output_in_sbuf=True),
+        dict(transposed_in=True),
+        dict(mode=ct.ComputationMode.DECODE),
+        dict(dtype_mode=ct.DtypeMode.NON_OCP),
+        dict(output_dtype=torch.float32),
+        dict(down_in_scale=torch.ones(1)),
+    ]
+    for over in bad:
+        with pytest.raises(NotImplementedError):
+            pkg.kernels.mlp(x, w, w, w, **_wan_mlp_kwargs(pkg, **over))
+    with pytest.raises(ValueError, match="MXWeight or a packed"):
+        pkg.kernels.mlp(x, torch.zeros(K, N), torch.zeros(K, N), w, **_wan_mlp_kwargs(pkg))
+    # the supported configuration with host tensors reaches the device check
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.kernels.mlp(x, w, w, w, **_wan_mlp_kwargs(pkg))
+
+
+def test_kernel_qkv_shim_rejections(pkg):
+    ct = pkg.common_types
+    x = torch.zeros(1, M, K + 4, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    wt = torch.zeros(K // 4, 3 * 128, 4, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="d_head"):
+        pkg.kernels.torch_compatible_row_mx_qkv(x, wt, torch.ones(1, 384))
+    with pytest.raises(NotImplementedError, match="replica"):
+        pkg.kernels.torch_compatible_row_mx_qkv(x, wt, torch.ones(1, 384), None, 128, 1, 1, replica_groups=((0, 1),))
+    with pytest.raises(NotImplementedError):
+        pkg.kernels.torch_compatible_row_mx_qkv(x, wt, torch.ones(1, 384), None, 128, 1, 1,
+                                                qk_norm_pre_rope_q_norm=ct.NormType.RMS_NORM)
+
+
+@pytest.mark.parametrize("head_dim", [64, 112, 256])
+def test_rope_refuses_head_dims_whose_split_disagrees(pkg, head_dim):
+    """rope.py builds axis tables 2*(hd//6) wide and slices them at hd//3 (rope.py:54-55, 91-95);
+    where those differ the reference's tables are not per-pair rotations, so these are refused."""
+    with pytest.raises(NotImplementedError, match="split"):
+        pkg.rope_tables((1, 2, 3), head_dim=head_dim, device="cpu")
+    with pytest.raises(NotImplementedError, match="split"):
+        pkg.WanRotaryPosEmbed(head_dim, (1, 2, 2), 1024)
+    pkg.WanRotaryPosEmbed(128, (1, 2, 2), 1024)  # the Wan head_dim is accepted

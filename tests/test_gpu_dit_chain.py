@@ -67,6 +67,9 @@ def test_three_block_chain(pkg, dev):
         h, _ = blockcheck.check_block_rows(pkg, w, h, td, rope, cr, torch.arange(S), GRID, fails=fails)
     assert not fails, fails
     assert torch.equal(blk.dit_forward(blocks, h0.to(dev), td, rope, crosses), h)
+    # given the latent grid, the forward builds the same tables itself (once per forward, as the
+    # reference's forward calls its rotary embedding)
+    assert torch.equal(blk.dit_forward(blocks, h0.to(dev), td, GRID, crosses), h)
 
     # the oracle's chains from the same latent: exact softmax, and the reference attention kernel's
     # own rounding points (bf16 P, bf16 pre-scaled Q, fp16 shifted scores)

@@ -255,3 +255,85 @@ def test_row_mx_o_proj(pkg, dev):
     ref = og.mx_gemm(xc, xs, codes.numpy(), np.full((dim, nh * HD // 32), 127, np.uint8), bias=bo.numpy(),
                      col_scale=np.full(dim, so, np.float32))
     _close(out.cpu().view(B * S, dim), ref, "row_mx_o_proj")
+
+
+def test_torch_compatible_row_mx_qkv(pkg, dev, qkv_case):
+    """The kernel-level QKV shim (qkv_shim.py:26-77) with the QK norm as flat scalars, as
+    ``row_mx_qkv_proj`` calls it (row_mx_kernels.py:91-111): the reference's packed de-interleaved
+    weight, rotate-half caches, both norms across heads; the result must be the oracle's, and
+    bit-identical to the same projection through ``row_mx_qkv_proj``."""
+    c = qkv_case
+    dim, order = c["dim"], c["order"]
+    ct = pkg.common_types
+    w = _pack(c["w_ref"]).to(dev)
+    scales, bias = c["scales"][order].to(dev)[None], c["bias"][order].to(dev)[None]
+    gq, gk = c["gq"][order[:dim]].to(dev)[None], c["gk"][order[dim : 2 * dim] - dim].to(dev)[None]
+    out = pkg.kernels.torch_compatible_row_mx_qkv(
+        hidden=c["packed"], qkv_weights=w, qkv_w_scale=scales, bias=bias, d_head=HD, num_q_heads=c["nh"],
+        num_kv_heads=c["nh"], output_layout=ct.QKVOutputLayout.BSD, fused_rope=True,
+        cos_cache=c["cos_cache"].to(dev), sin_cache=c["sin_cache"].to(dev),
+        qk_norm_pre_rope_q_norm=ct.NormType.RMS_NORM_ACROSS_HEADS,
+        qk_norm_pre_rope_k_norm=ct.NormType.RMS_NORM_ACROSS_HEADS, qk_norm_pre_rope_eps=1e-6,
+        qk_norm_pre_rope_q_gamma=gq, qk_norm_pre_rope_k_gamma=gk, replica_groups=None,
+    )
+    assert out.shape == (c["B"], c["S"], 3 * dim)
+    ref = c["ref_nat"][..., order]
+    got = out.cpu()
+    for name, sl in (("Q", slice(0, dim)), ("K", slice(dim, 2 * dim)), ("V", slice(2 * dim, 3 * dim))):
+        for b in range(c["B"]):
+            _close(got[b, :, sl], ref[b, :, sl], f"shim {name} batch {b}")
+    via = _call_self(pkg, c, dev, w, None, c["scales"][order], c["bias"][order], c["gq"][order[:dim]],
+                     c["gk"][order[dim : 2 * dim] - dim])
+    assert torch.equal(out, via)
+    # no norm given: the plain ROW_MX projection in NBSd
+    plain = pkg.kernels.torch_compatible_row_mx_qkv(
+        c["packed"], w, scales, bias, HD, c["nh"], c["nh"], ct.QKVOutputLayout.NBSd)
+    lin = c["lin"][..., order]
+    for b in range(c["B"]):
+        _close(plain[:, b].permute(1, 0, 2).reshape(c["S"], 3 * dim).cpu(), lin[b], f"shim plain batch {b}")
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_kernel_mlp_wan_configuration(pkg, dev, batched):
+    """The nkilib ``mlp`` kernel signature (mlp.py:53) in exactly the configuration the Wan FFN
+    launches (row_mx_kernels.py:172-198: gate-less, GELU-tanh, ROW_MX, gate tensors aliasing the up
+    tensors, the up bias in the reference's tiled [128, tiles, 4] form, the down bias [1, H], the
+    down scale partition-expanded), against the oracle's ROW_MX MLP; the packed [K/4, N, 4] weights
+    are taken as the reference passes them. Returns a one-element list, [B, S, H]."""
+    ct = pkg.common_types
+    S, dim, ffn = 260, 1024, 2816
+    g = torch.Generator().manual_seed(21)
+    h = torch.randn(S, dim, generator=g).to(torch.bfloat16)
+    wu, su = _per_tensor_fp8(torch.randn(dim, ffn, generator=g) * 0.02)
+    wd, sd = _per_tensor_fp8(torch.randn(ffn, dim, generator=g) * 0.02)
+    bu, bd = 0.1 * torch.randn(ffn, generator=g), 0.1 * torch.randn(dim, generator=g)
+    packed = pkg.adaln_modulate(h.to(dev), eps=1e-6, quant="row")
+    if batched:
+        packed = packed.view(2, S // 2, dim + 4)
+    tiles = (ffn + 511) // 512
+    bu_tiled = torch.nn.functional.pad(bu, (0, tiles * 512 - ffn)).reshape(tiles, 128, 4).permute(1, 0, 2).contiguous()
+    up_w, down_w = _pack(wu).to(dev), _pack(wd).to(dev)
+    up_s, down_s = torch.full((1, ffn), su, device=dev), torch.full((128, dim), sd, device=dev)
+    res = pkg.kernels.mlp(
+        hidden_tensor=packed, gate_proj_weights_tensor=up_w, up_proj_weights_tensor=up_w,
+        down_proj_weights_tensor=down_w, normalization_weights_tensor=None, gate_proj_bias_tensor=bu_tiled.to(dev),
+        up_proj_bias_tensor=bu_tiled.to(dev), down_proj_bias_tensor=bd.to(dev)[None], normalization_bias_tensor=None,
+        fused_add_tensor=None, store_fused_add_result=False, activation_fn=ct.ActFnType.GELU_Tanh_Approx,
+        normalization_type=ct.NormType.NO_NORM, quantization_type=ct.QuantizationType.ROW_MX, gate_w_scale=up_s,
+        up_w_scale=up_s, down_w_scale=down_s, gate_up_in_scale=None, down_in_scale=None, quant_clipping_bound=None,
+        output_dtype="bfloat16", store_output_in_sbuf=False, eps=1e-6, skip_gate_proj=True,
+        use_tkg_gate_up_proj_column_tiling=False, use_tkg_down_proj_column_tiling=False,
+        use_tkg_down_proj_optimized_layout=False, gate_clamp_upper_limit=None, gate_clamp_lower_limit=None,
+        up_clamp_upper_limit=None, up_clamp_lower_limit=None, force_cte_mode=True, dtype_mode=ct.DtypeMode.AUTO,
+        gate_up_w_layout=ct.MLPGateUpWeightLayout.H_X4_INNERMOST,
+    )
+    assert isinstance(res, list) and len(res) == 1
+    out = res[0]
+    assert out.shape == ((2, S // 2, dim) if batched else (1, S, dim)) and out.dtype == torch.bfloat16
+    up = _row_mx_oracle(packed, wu, np.full(ffn, su, np.float32), bu.numpy())
+    gel = og.gelu_tanh(up).float().to(torch.bfloat16).float().numpy()
+    ic, isc = omx.mx_quantize(gel)
+    wdc = wd.view(torch.uint8).t().contiguous().numpy()
+    ref = og.mx_gemm(ic, isc, wdc, np.full((dim, ffn // 32), 127, np.uint8), bias=bd.numpy(),
+                     col_scale=np.full(dim, sd, np.float32))
+    _close(out.cpu().view(S, dim), ref, "kernels.mlp")

@@ -217,14 +217,16 @@ def test_gemm_full_mlp_shapes_row_subset(pkg, dev):
     assert bool((err <= bound + 1e-30).all())
 
 
+@pytest.mark.parametrize("K", [640, 1024])
 @pytest.mark.parametrize("M", [300, 1560, 4100])
-def test_qkv_projection_writes_v_transposed(pkg, dev, M):
+def test_qkv_projection_writes_v_transposed(pkg, dev, M, K):
     """``mxfp8_qkv_linear``: the Q|K columns bit-identical to the plain GEMM's, the Q sums of squares
     identical, and the V columns written as V^T in the attention's key order -- against
-    ``transpose_heads`` of the plain GEMM's V (zero past the last token) within one bf16 rounding (its MFMAs take the operands in the other order, so the fp32 accumulation may round
-    differently)."""
+    ``transpose_heads`` of the plain GEMM's V (zero past the last token) within one bf16 rounding (its
+    MFMAs take the operands in the other order, so the fp32 accumulation may round differently).
+    K = 640 runs the simple-loop kernel, K = 1024 (a multiple of 512) the pipelined ring kernel."""
     dim = 1024
-    xq, wq, _, _ = _operands(pkg, dev, M, 3 * dim, 640, seed=M)
+    xq, wq, _, _ = _operands(pkg, dev, M, 3 * dim, K, seed=M + K)
     ss_ref = torch.empty(M, 3 * dim // 128, device=dev)
     full = pkg.mxfp8_linear(xq, wq, row_sumsq=ss_ref, sumsq_cols=dim)
     ss = torch.full((M, 2 * dim // 128), float("nan"), device=dev)
@@ -235,5 +237,6 @@ def test_qkv_projection_writes_v_transposed(pkg, dev, M):
     d = (vt.float() - vt_ref.float()).abs()
     assert bool((d <= 2.0**-8 * vt_ref.float().abs()).all()), float(d.max())
     assert float((d > 0).float().mean()) < 1e-3
+    assert not bool(vt[:, :, M:].any()), "V^T padding past the last token must be zero"
     assert torch.equal(ss[:, : dim // 128], ss_ref[:, : dim // 128])
     assert bool(torch.isnan(ss[:, dim // 128 :]).all())

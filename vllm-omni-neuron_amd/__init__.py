@@ -34,3 +34,4 @@ from .attention_ops import (  # noqa: F401
 attention_ops.register_torch_ops()
 from . import block  # noqa: F401
 from . import comfy_fp8_checkpoint  # noqa: F401
+from . import kernels  # noqa: F401

@@ -34,6 +34,7 @@ import torch
 
 from . import attention_ops as ops
 from .adaln_kernels import adaln_quant_2d
+from .rope import rope_tables
 from .row_mx_kernels import MXWeight, mxfp8_linear, mxfp8_qkv_linear, quantize_weight_mx
 
 DIM, HEADS, HEAD_DIM, FFN = 5120, 40, 128, 13824
@@ -170,9 +171,18 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
 
 def dit_forward(blocks, h: torch.Tensor, temb: torch.Tensor, rope, crosses, eps: float = 1e-6, timer=None,
                 tables: torch.Tensor | None = None):
-    """The 40-block loop of one DiT forward (one CFG branch), cross-attention K/V cached. The
-    modulation rows of every block are formed in one batched op up front; ``tables`` optionally
-    holds the blocks' stacked ``scale_shift_table`` ``[B, 6, DIM]`` (built here otherwise)."""
+    """The 40-block loop of one DiT forward (one CFG branch), cross-attention K/V cached. ``rope``
+    is either the ``(cos, sin)`` pair tables ``[S, 64]`` or the latent patch grid ``(F, H, W)``; given
+    the grid, the tables are built here, once per forward, as the reference's forward calls its
+    rotary embedding (wan2_2_transformer.py:1757). The modulation rows of every block are formed in
+    one batched op up front; ``tables`` optionally holds the blocks' stacked ``scale_shift_table``
+    ``[B, 6, DIM]`` (built here otherwise)."""
+    run = timer or (lambda name, fn: fn())
+    if len(rope) == 3 and all(isinstance(v, int) for v in rope):
+        grid = tuple(rope)
+        if grid[0] * grid[1] * grid[2] != h.shape[0]:
+            raise ValueError(f"grid {grid} holds {grid[0] * grid[1] * grid[2]} tokens, h has {h.shape[0]}")
+        rope = run("rope_tables", lambda: rope_tables(grid, device=h.device))
     if tables is None:
         tables = torch.stack([w.scale_shift_table for w in blocks])
     mods = modulation(tables, temb)

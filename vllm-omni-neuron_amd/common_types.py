@@ -41,6 +41,34 @@ class QKVOutputLayout(enum.Enum):
     NBSd = "nbsd"  # [N, B, S, d]
 
 
+class ActFnType(enum.Enum):
+    """MLP activation (reference ActFnType); Wan's FFN uses the tanh-approximated GELU."""
+
+    SiLU = "silu"
+    GELU = "gelu"
+    GELU_Tanh_Approx = "gelu_tanh_approx"
+    Swish = "swish"
+    ReLU = "relu"
+    SquaredReLU = "squared_relu"
+
+
+class MLPGateUpWeightLayout(enum.Enum):
+    """How the reference lays out the MLP up/gate weight for its kernel. Here every weight is an
+    :class:`MXWeight` or a packed ``[K/4, N, 4]`` tensor; the member only documents the caller's
+    intent and is accepted for signature compatibility."""
+
+    CONTIGUOUS = "contiguous"
+    H_X4_INNERMOST = "h_x4_innermost"
+
+
+class ComputationMode(enum.Enum):
+    """Reference MLP dispatch mode: context encoding (PREFILL) or token generation (DECODE)."""
+
+    AUTO = "auto"
+    PREFILL = "prefill"
+    DECODE = "decode"
+
+
 class QKNormConfig(NamedTuple):
     """Across-heads RMSNorm applied to Q and/or K before RoPE (reference QKNormConfig)."""
 

@@ -1141,6 +1141,11 @@ extern "C" int wanmi_mxfp8_gemm_qkv(const uint8_t* a_codes, const uint8_t* a_sca
   WANMI_REQUIRE(sumsq_cols >= 0 && sumsq_cols <= vt_col0 && sumsq_cols % 128 == 0, WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm_qkv: sumsq_cols=%lld must be a multiple of 128 in [0, vt_col0]", (long long)sumsq_cols);
   WANMI_REQUIRE(K % 32 == 0, WANMI_ERR_ARG, "wanmi_mxfp8_gemm_qkv: K=%lld must be a multiple of 32", (long long)K);
+  // The V^T epilogue writes the token columns of the 256-token tiles it covers (zeros past M), so
+  // padding past M is only written up to M rounded up to 256; with M == 0 nothing would be written.
+  WANMI_REQUIRE(M > 0 && vt_ld <= (M + TM - 1) / TM * TM, WANMI_ERR_ARG,
+                "wanmi_mxfp8_gemm_qkv: M=%lld must be positive and vt_ld=%lld at most M rounded up to %d",
+                (long long)M, (long long)vt_ld, TM);
   // Q | K: the plain bf16 epilogue (with the Q partial sums) on the weight rows [0, vt_col0)
   int st = gemm_impl(a_codes, a_scales, w_codes, w_scales, row_scale, col_scale, bias, M, vt_col0, K, lda,
                      WANMI_EPI_BF16, out, ldo, nullptr, nullptr, nullptr, row_sumsq, row_sumsq ? sumsq_cols : 0,

@@ -72,6 +72,12 @@ extern "C" int wanmi_rope_tables(int64_t frames, int64_t height, int64_t width, 
                 "wanmi_rope_tables: head_dim=%d must be even and at most %d", head_dim, 2 * kMaxRopePairs);
   WANMI_REQUIRE(head_dim >= 6, WANMI_ERR_ARG, "wanmi_rope_tables: head_dim=%d leaves an axis without channels",
                 head_dim);
+  // rope.py builds the axis tables 2 * (head_dim / 6) wide but its forward slices them at head_dim / 3
+  // (rope.py:54-55 against 91-95); where the two differ its slices cut pairs apart, which no per-pair
+  // table reproduces
+  WANMI_REQUIRE(head_dim / 3 == 2 * (head_dim / 6), WANMI_ERR_UNSUPPORTED,
+                "wanmi_rope_tables: head_dim=%d: the reference's axis widths (%d) and forward split (%d) disagree",
+                head_dim, 2 * (head_dim / 6), head_dim / 3);
   WANMI_REQUIRE(frames >= 0 && height >= 0 && width >= 0 && max_seq_len <= (1LL << 20), WANMI_ERR_ARG,
                 "wanmi_rope_tables: grid sizes must be non-negative and max_seq_len at most 2^20");
   WANMI_REQUIRE(frames <= max_seq_len && height <= max_seq_len && width <= max_seq_len, WANMI_ERR_ARG,

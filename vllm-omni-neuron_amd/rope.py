@@ -22,6 +22,18 @@ from . import _lib
 _LAYOUT = {"pairs": 0, "interleaved": 1, "rotate_half": 2}
 
 
+def _check_axis_split(head_dim: int) -> None:
+    """The reference builds its axis tables with widths ``[hd - 4 (hd // 6), 2 (hd // 6), 2 (hd // 6)]``
+    (rope.py:54-55) but slices them in ``forward`` at ``[hd - 2 (hd // 3), hd // 3, hd // 3]``
+    (rope.py:91-95). The two agree only when ``hd // 3 == 2 (hd // 6)`` (every even head_dim except
+    those of the form 6k + 4, such as 64, 112 and 256); otherwise the reference's slices cut pairs
+    apart and mix axes, which no per-pair table reproduces, so such head_dims are refused."""
+    if head_dim // 3 != 2 * (head_dim // 6):
+        raise NotImplementedError(
+            f"head_dim={head_dim}: the reference's axis widths 2*(head_dim//6)={2 * (head_dim // 6)} and its forward's "
+            f"split head_dim//3={head_dim // 3} disagree; only head_dims where they agree (e.g. 128) are built")
+
+
 def rope_tables(grid, *, head_dim: int = 128, max_seq_len: int = 1024, theta: float = 10000.0,
                 layout: str = "pairs", device="cuda"):
     """``(cos, sin)`` fp32 for the latent patch grid ``(F, H, W)`` in raster order: ``[S, head_dim/2]``
@@ -29,6 +41,7 @@ def rope_tables(grid, *, head_dim: int = 128, max_seq_len: int = 1024, theta: fl
     freqs layout; ``"rotate_half"``: ``cat([base, base])``)."""
     if layout not in _LAYOUT:
         raise ValueError(f"unknown layout {layout!r}")
+    _check_axis_split(head_dim)
     F_, H_, W_ = (int(v) for v in grid)
     if min(F_, H_, W_) < 0:
         raise ValueError(f"grid sizes must be non-negative, got {grid}")
@@ -54,6 +67,7 @@ class WanRotaryPosEmbed(torch.nn.Module):
     def __init__(self, attention_head_dim: int, patch_size: tuple[int, int, int], max_seq_len: int,
                  theta: float = 10000.0):
         super().__init__()
+        _check_axis_split(attention_head_dim)
         self.attention_head_dim = attention_head_dim
         self.patch_size = tuple(patch_size)
         self.max_seq_len = max_seq_len

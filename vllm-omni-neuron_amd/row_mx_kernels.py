@@ -264,6 +264,9 @@ def mxfp8_qkv_linear(x, weight: MXWeight, *, vt_col0: int, row_sumsq: torch.Tens
     dev = codes.device
     s_pad = (max(M, 1) + 63) // 64 * 64
     qk = torch.empty((M, vt_col0), dtype=torch.bfloat16, device=dev)
+    if M == 0:  # no tokens: nothing to project, V^T is all padding
+        return qk.reshape(*lead, vt_col0), torch.zeros(((N - vt_col0) // head_dim, head_dim, s_pad),
+                                                       dtype=torch.bfloat16, device=dev)
     vt = torch.empty(((N - vt_col0) // head_dim, head_dim, s_pad), dtype=torch.bfloat16, device=dev)
     status = lib.wanmi_mxfp8_gemm_qkv(
         _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(weight.codes), _lib.ptr(weight.scales), _lib.ptr(row_scale),
