@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define WANMI_ABI_VERSION 2
+#define WANMI_ABI_VERSION 3
 
 #define WANMI_OK 0
 #define WANMI_ERR_ARG (-1)         /* bad pointer / size / enum argument */
@@ -225,6 +225,25 @@ int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_stride, int64_
                                     int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
                                     const float* q_sumsq, int64_t q_sumsq_ld, const float* q_gamma,
                                     const float* q_cos, const float* q_sin, float q_eps, void* stream);
+
+/*
+ * Exact-softmax attention for the drop-ins of a running-max flash attention: the reference's
+ * registered attention_cte op and _nki_attend (vllm_omni_neuron/diffusion/models/wan2_2/
+ * wan2_2_transformer.py:83-108, 165-171, 653-674), which wan_cp_self_attention runs on one device
+ * (806-847). Runs wanmi_attention_const_max (arguments as there; out_mode TOKEN or DMAJOR only, the
+ * bf16 layouts those drop-ins return) writing every query's row sum of P to row_sum [heads][Sq] fp32,
+ * then recomputes every row whose sum is below 2^-96 (the constant-max bound exceeded the row's
+ * largest logit by so much that its P underflowed, or the sum is NaN) with the row's true max, in
+ * fp32: o = sum_j exp(s q.k_j - m) v_j / sum_j exp(s q.k_j - m), m = max_j s q.k_j. Rows at or above
+ * 2^-96 keep the constant-max result, which is then within bf16 rounding of the softmax. Two
+ * launches on `stream`; row_sum is scratch the caller owns (its contents on return are the
+ * constant-max row sums).
+ */
+int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64_t q_token_stride, const void* k,
+                          int64_t k_head_stride, int64_t k_token_stride, const void* vt, int64_t vt_ld,
+                          const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
+                          int out_mode, void* out, int64_t o_head_stride, int64_t o_token_stride,
+                          int64_t o_d_stride, float* row_sum, void* stream);
 
 /*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,

@@ -1,12 +1,15 @@
 """The Wan transformer block composed from the oracle pieces -- test infrastructure only.
 
-Two restatements of ``WanTransformerBlock.forward`` (vllm_omni_neuron/diffusion/models/wan2_2/
+Three restatements of ``WanTransformerBlock.forward`` (vllm_omni_neuron/diffusion/models/wan2_2/
 wan2_2_transformer.py:1428-1513):
 
 - :func:`mxfp8_block`: the MXFP8 recipe at exactly the quantization points the GPU path uses
   (MX activations from the canonical adaLN, MX weights, bf16 projection outputs, bf16 q/k/v,
   MX attention output and GELU intermediate). GEMMs run in fp32 on dequantized operands (exact
   products; fp32 accumulation, far inside the bf16 tolerance); attention is exact softmax in fp64.
+- :func:`row_mx_block`: the reference's own FP8 recipe, ROW activations at every adaLN site and
+  per-tensor FP8 checkpoint weights with per-channel scales (the ROW_MX modules of
+  row_mx_modules.py), MX re-quantization of the attention outputs and of the GELU intermediate.
 - :func:`bf16_eager_block`: the reference's BF16 eager fallback chain -- ``_eager_adaln``
   (adaln_kernels.py:51-84), ``torch.matmul`` projections (wan2_2_transformer.py:1104),
   ``DistributedRMSNorm`` (879-893), ``apply_rotary_emb_wan`` (rope.py:8-34), ``_torch_attend``
@@ -128,6 +131,78 @@ def mxfp8_block(raw, wq, h, temb, context, grid, eps=1e-6, attend=None):
     out = _bf16(h2 + ffn * c_gate)
     return {"a1_codes": a1["codes"], "a1_scales": a1["scales"], "qkv": qkv, "attn1": attn1, "h1": h1,
             "attn2": attn2, "h2": h2, "inter": g, "out": out}
+
+
+def _row_lin(codes, dq, ck, bias) -> torch.Tensor:
+    """The ROW_MX projection of a ROW-quantized activation (codes [T, K] uint8, per-row dq [T, 1])
+    with a per-tensor FP8 checkpoint weight ``ck = (codes [K, N] e4m3fn, per-channel scale [N])``:
+    ``bf16((codes . W_codes) * dq * c + b)`` (qkv_cte.py:3996-4021), fp32 accumulation."""
+    a = torch.from_numpy(omx.e4m3_decode(np.asarray(codes)).astype(np.float32))
+    y = (a @ ck[0].float()) * torch.as_tensor(np.asarray(dq, np.float32)).reshape(-1, 1) * ck[1].float().reshape(1, -1)
+    return _bf16(y + bias.float())
+
+
+def _mx_lin(a_codes, a_scales, ck, bias) -> torch.Tensor:
+    """An MX activation against a per-tensor FP8 checkpoint weight: ``bf16((A_deq . W_codes) * c + b)``."""
+    y = (_deq(a_codes, a_scales) @ ck[0].float()) * ck[1].float().reshape(1, -1)
+    return _bf16(y + bias.float())
+
+
+def row_mx_block(raw, ckpt, h, temb, context, grid, eps=1e-6, attend=None):
+    """The reference's FP8 recipe with ROW activations (``_leaf_quant`` = "row", T:1423-1426), in
+    natural channel order, on CPU: every adaLN site row-quantizes (per-row ``amax / 448`` scale),
+    the projections are ROW_MX (codes x FP8 checkpoint codes x row scale x channel scale + bias),
+    the o-projections MX-quantize their attention input (row_mx_o_proj), the FFN up projection is
+    followed by GELU-tanh, bf16 and MX (mlp_torch.py:586-594), and the block ends with the gated add
+    (T:1508-1512). ``ckpt``: projection name (``qkv``, ``o``, ``q2``, ``k2``, ``v2``, ``o2``, ``up``,
+    ``down``) -> (codes [K, N] e4m3fn, per-channel scale [N]); ``raw`` as :func:`mxfp8_block`.
+    Returns the intermediates (``a1_packed``, ``qkv``, ``attn1``, ``h1``, ``attn2``, ``h2``,
+    ``inter``) and ``out``."""
+    attend = attend or _attend
+    S, dim = h.shape
+    heads = dim // HEAD_DIM
+    scale = HEAD_DIM**-0.5
+    e = raw["scale_shift_table"].float() + temb.reshape(6, dim).float()
+    shift, sc, gate, c_shift, c_sc, c_gate = (e[i] for i in range(6))
+    cos, sin = orope.wan_rope(grid)
+    hn = h.float().numpy()
+
+    a1 = oadaln.adaln_quant(hn, (1 + sc).numpy(), shift.numpy(), eps=eps, quant="row")
+    qkv = _row_lin(a1["codes"], a1["dq"], ckpt["qkv"], raw["qkv_b"])
+    q = orope.rms_norm_across_heads(qkv[:, :dim].to(torch.bfloat16), raw["norm_q"], eps).view(1, S, heads, HEAD_DIM)
+    k = orope.rms_norm_across_heads(qkv[:, dim : 2 * dim].to(torch.bfloat16), raw["norm_k"], eps).view(1, S, heads, HEAD_DIM)
+    q = orope.apply_rotary_emb_wan(q, cos[None, :, None], sin[None, :, None])[0]
+    k = orope.apply_rotary_emb_wan(k, cos[None, :, None], sin[None, :, None])[0]
+    v = qkv[:, 2 * dim :].to(torch.bfloat16).view(S, heads, HEAD_DIM)
+    o1 = attend(q, k, v, scale)
+    o1c, o1s = _mx_of(o1)
+    attn1 = _mx_lin(o1c, o1s, ckpt["o"], raw["o_b"])
+
+    r2 = oadaln.adaln_quant(attn1.numpy(), raw["norm2_weight"].numpy(), raw["norm2_bias"].numpy(), eps=eps,
+                            quant="row", residual=hn, gate=gate.numpy())
+    h1 = torch.from_numpy(r2["residual_out"])
+    q2 = _row_lin(r2["codes"], r2["dq"], ckpt["q2"], raw["q2_b"])
+    q2 = orope.rms_norm_across_heads(q2.to(torch.bfloat16), raw["norm_q2"], eps).view(S, heads, HEAD_DIM)
+    cc, cdq = omx.row_quantize(context.float().numpy())
+    k2 = orope.rms_norm_across_heads(_row_lin(cc, cdq, ckpt["k2"], raw["k2_b"]).to(torch.bfloat16), raw["norm_k2"], eps)
+    v2 = _row_lin(cc, cdq, ckpt["v2"], raw["v2_b"]).to(torch.bfloat16)
+    St = context.shape[0]
+    o2 = attend(q2, k2.view(St, heads, HEAD_DIM), v2.view(St, heads, HEAD_DIM), scale)
+    o2c, o2s = _mx_of(o2)
+    attn2 = _mx_lin(o2c, o2s, ckpt["o2"], raw["o2_b"])
+
+    r3 = oadaln.adaln_quant(attn2.numpy(), (1 + c_sc).numpy(), c_shift.numpy(), eps=eps, quant="row",
+                            residual=h1.numpy(), gate=None)
+    h2 = torch.from_numpy(r3["residual_out"])
+    a3 = torch.from_numpy(omx.e4m3_decode(r3["codes"]).astype(np.float32))
+    up = (a3 @ ckpt["up"][0].float()) * torch.from_numpy(r3["dq"]).reshape(-1, 1) * ckpt["up"][1].float() \
+        + raw["up_b"].float()
+    g = torch.from_numpy(bf16_round(F.gelu(up, approximate="tanh").numpy()))
+    gc, gs = _mx_of(g)
+    ffn = _mx_lin(gc, gs, ckpt["down"], raw["down_b"])
+    out = _bf16(h2 + ffn * c_gate)
+    return {"a1_packed": a1["packed"], "qkv": qkv, "attn1": attn1, "h1": h1, "attn2": attn2, "h2": h2, "inter": g,
+            "out": out}
 
 
 def bf16_eager_block(raw, h, temb, context, grid, eps=1e-6):

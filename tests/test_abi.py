@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol(pkg):
 def test_abi_version_and_error_reporting(pkg):
     lib = pkg._lib.load()
     header = (ROOT / "include" / "wanmi.h").read_text()
-    assert lib.wanmi_abi_version() == int(re.search(r"WANMI_ABI_VERSION (\d+)", header).group(1)) == 2
+    assert lib.wanmi_abi_version() == int(re.search(r"WANMI_ABI_VERSION (\d+)", header).group(1)) == 3
     # an argument error is reported without touching the GPU
     st = lib.wanmi_adaln_quant(None, None, None, None, None, 4, 100, 1e-6, 1, 1, None, None, None, None)
     assert st == pkg._lib.WANMI_ERR_ARG

@@ -258,3 +258,49 @@ def test_dropins_match_reference_layouts(pkg, dev):
     _check_attn(o4.cpu().transpose(1, 2), ref4)
     with pytest.raises(NotImplementedError):
         ops.wan_cp_self_attention(q.to(dev), k.to(dev), v.to(dev), s, 2, None, None)
+
+
+def _loose_bound_case(B, N, Sq, Sk, seed):
+    """Inputs whose constant-max bound c = s ||q|| max||k|| is far above many rows' largest logit:
+    key 0 of every head has norm 400 along d = 0 while the other keys are N(0, 1); even query rows
+    have norm ~100 orthogonal to d = 0 (their true largest logit is ~30 below... c ~ 3500: every P
+    of the row underflows), odd rows lie along d = 0 (c equals their logit with key 0: no
+    underflow). A constant-max kernel returns the even rows as zero."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Sq, N, 128, generator=g) * 9.0
+    q[:, 0::2, :, 0] = 0.0
+    q[:, 1::2] = 0.05 * q[:, 1::2]
+    q[:, 1::2, :, 0] = 50.0
+    k = torch.randn(B, Sk, N, 128, generator=g)
+    k[:, 0] = 0.0
+    k[:, 0, :, 0] = 400.0
+    v = torch.randn(B, Sk, N, 128, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("Sk", [500, 1900])
+def test_exact_dropins_survive_a_loose_bound(pkg, dev, Sk):
+    """The drop-ins of the reference's running-max attention (``_nki_attend``, the registered
+    ``attention_cte`` op, ``wan_cp_self_attention``) give the softmax even where the constant-max
+    bound exceeds a row's largest logit by thousands (every P of the row underflows): those rows are
+    recomputed with the row's true max. 500 keys run the head-group kernel, 1900 the one-head kernel.
+    Bars as the other attention tests, against fp64 softmax."""
+    ops = pkg.attention_ops
+    B, N, Sq = 1, 8, 150
+    s = 128**-0.5
+    q, k, v = _loose_bound_case(B, N, Sq, Sk, seed=Sk)
+    ref = oa.torch_attend(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), s, dtype=torch.float64)
+    assert float(ref[:, :, 0::2].abs().max()) > 0.1  # the underflowing rows are not zero in the softmax
+    # the plain constant-max kernel indeed loses the even rows (what the rescue is for)
+    vt, _ = ops.transpose_heads(v[0].to(dev))
+    plain = ops.attention_core(q[0].to(dev), k[0].to(dev), vt, ops.head_max_norm(k[0].to(dev)), s).cpu()
+    assert float(plain.view(Sq, N, 128)[0::2].float().abs().max()) == 0.0
+    o1 = ops._nki_attend(q.transpose(1, 2).to(dev), k.transpose(1, 2).to(dev), v.transpose(1, 2).to(dev), s).cpu()
+    _check_attn(o1.transpose(2, 3), ref)
+    o2 = ops.wan_cp_self_attention(q.to(dev), k.to(dev), v.to(dev), s, 1, None, None).cpu()
+    _check_attn(o2.transpose(2, 3), ref)
+    qb, kb, vb = (t.transpose(1, 2).reshape(B * N, -1, 128) for t in (q, k, v))
+    qs = (qb.float() * s).to(torch.bfloat16)
+    o3 = torch.ops.wan_transformer.attention_cte(qs.to(dev), kb.to(dev), vb.to(dev)).cpu()
+    ref3 = oa.torch_attend(qs[None], kb[None], vb[None], 1.0, dtype=torch.float64)[0]
+    _check_attn(o3.transpose(1, 2), ref3)

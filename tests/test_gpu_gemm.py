@@ -237,6 +237,10 @@ def test_qkv_projection_writes_v_transposed(pkg, dev, M, K):
     d = (vt.float() - vt_ref.float()).abs()
     assert bool((d <= 2.0**-8 * vt_ref.float().abs()).all()), float(d.max())
     assert float((d > 0).float().mean()) < 1e-3
-    assert not bool(vt[:, :, M:].any()), "V^T padding past the last token must be zero"
+    # slot r of a 16-key group holds key (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1): the padding is
+    # the slots whose key is >= M (not simply the slots >= M when M is not a multiple of 16)
+    slots = torch.arange(vt.shape[-1])
+    key = (slots & ~15) | (slots & 3) | ((slots & 4) << 1) | ((slots & 8) >> 1)
+    assert not bool(vt[:, :, (key >= M).to(dev)].any()), "V^T padding past the last token must be zero"
     assert torch.equal(ss[:, : dim // 128], ss_ref[:, : dim // 128])
     assert bool(torch.isnan(ss[:, dim // 128 :]).all())

@@ -79,3 +79,41 @@ def test_planted_composition_slips_are_far_outside_the_quantization_gap():
         raw_t = dict(raw)
         c = _cos_update(ob.mxfp8_block(raw_t, wq, h, t, ctx, GRID)["out"], eager, h)
         assert c < base - 0.05, (name, c, base)
+
+
+def _checkpoint(raw):
+    """Per-tensor FP8 checkpoint weights (codes [K, N] e4m3fn of w / s, s = amax / 448, expanded per
+    channel), the fused QKV as its three Q, K, V tensors with three scalars."""
+    def quant(w):
+        s = w.float().abs().max() / 448.0
+        return (w.float() / s).to(torch.float8_e4m3fn), s
+
+    ck = {}
+    parts = [quant(raw["qkv_w"][:, i * DIM : (i + 1) * DIM]) for i in range(3)]
+    ck["qkv"] = (torch.cat([c for c, _ in parts], 1), torch.cat([s.expand(DIM) for _, s in parts]))
+    for n in NAMES[1:]:
+        c, s = quant(raw[n + "_w"])
+        ck[n] = (c, s.expand(c.shape[1]))
+    return ck
+
+
+def test_row_recipe_block_agrees_with_the_eager_block():
+    """The ROW recipe (``row_mx_block``: ROW activations, per-tensor FP8 weights with per-channel
+    scales) against the independent BF16 eager chain: its update agrees within the quantization gap
+    (per-row activation scales lose more than per-32 block scales, so the bar is lower than the MX
+    recipe's), and the planted composition slips fall far below it."""
+    raw, _, h, temb, ctx = _setup()
+    ck = _checkpoint(raw)
+    eager = ob.bf16_eager_block(raw, h, temb, ctx, GRID)
+    r = ob.row_mx_block(raw, ck, h, temb, ctx, GRID)
+    base = _cos_update(r["out"], eager, h)
+    assert base >= 0.995, base
+    assert r["a1_packed"].shape == (h.shape[0], DIM + 4) and r["inter"].shape == (h.shape[0], FFN)
+    for name, t in {"shift<->scale": temb[[1, 0, 2, 3, 4, 5]], "gate<->c_gate": temb[[0, 1, 5, 3, 4, 2]],
+                    "c_shift<->shift": temb[[3, 1, 2, 0, 4, 5]]}.items():
+        c = _cos_update(ob.row_mx_block(raw, ck, h, t, ctx, GRID)["out"], eager, h)
+        assert c < base - 0.05, (name, c, base)
+    # a dropped channel scale (the weight codes taken as the weights) is far off as well
+    bad = {n: (c, torch.ones_like(s)) for n, (c, s) in ck.items()}
+    c = _cos_update(ob.row_mx_block(raw, bad, h, temb, ctx, GRID)["out"], eager, h)
+    assert c < base - 0.05, c

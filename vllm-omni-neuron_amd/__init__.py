@@ -35,3 +35,4 @@ attention_ops.register_torch_ops()
 from . import block  # noqa: F401
 from . import comfy_fp8_checkpoint  # noqa: F401
 from . import kernels  # noqa: F401
+from . import row_block  # noqa: F401

@@ -130,13 +130,22 @@ class QPrep(NamedTuple):
 
 
 def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: torch.Tensor, scale: float,
-                   out_mode: int = OUT_TOKEN, out: torch.Tensor | None = None, q_prep: QPrep | None = None):
+                   out_mode: int = OUT_TOKEN, out: torch.Tensor | None = None, q_prep: QPrep | None = None,
+                   exact: bool = False):
     """Constant-max attention on ``[S, N, 128]`` views q (Sq) and k (Sk), V^T from
     :func:`transpose_heads`. Returns token-major bf16 ``[Sq, N*128]``, d-major bf16
     ``[N, 128, Sq]`` or an :class:`MXTensor` ``[Sq, N*128]``. With ``q_prep`` q is the raw
     projection and the kernel applies the across-heads RMSNorm (and RoPE) to it on load, exactly as
-    :func:`qk_rmsnorm_rope_` would in a separate pass."""
+    :func:`qk_rmsnorm_rope_` would in a separate pass.
+
+    ``exact``: the semantics of a running-max softmax for any inputs (``wanmi_attention_exact``):
+    rows whose constant-max row sum underflowed (the bound exceeded the row's largest logit by more
+    than about 87) are recomputed with the row's true max. Token-major and d-major outputs only,
+    without ``q_prep``. The constant-max reference kernels (the ring attention and the block's own
+    path) do not do this."""
     lib = _lib.load()
+    if exact and (q_prep is not None or out_mode == OUT_MX):
+        raise ValueError("exact attention produces token-major or d-major bf16 output from prepared q")
     if q.dim() != 3 or k.dim() != 3 or q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
         raise ValueError("q, k must be bf16 [S, N, 128] views")
     Sq, N, D = q.shape
@@ -183,7 +192,11 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
         vt.shape[-1], _lib.ptr(kmax), Sq, Sk, N, D, float(scale), out_mode, _lib.ptr(out), o_hs, o_ss, o_ds,
         _lib.ptr(scales), 0 if scales is None else scales.stride(0),
     )
-    if q_prep is None:
+    if exact:
+        row_sum = torch.empty((N, Sq), dtype=torch.float32, device=dev)
+        st = lib.wanmi_attention_exact(*common[:-2], _lib.ptr(row_sum), _lib.stream_of(q))
+        _lib.check(st, "wanmi_attention_exact")
+    elif q_prep is None:
         st = lib.wanmi_attention_const_max(*common, _lib.stream_of(q))
         _lib.check(st, "wanmi_attention_const_max")
     else:
@@ -199,10 +212,11 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
     return out
 
 
-def _attend_bsnd(q, k, v, scale, out_mode):
-    """One batch element: q [Sq, N, D], k/v [Sk, N, D] (unit d stride)."""
+def _attend_bsnd(q, k, v, scale, out_mode, exact):
+    """One batch element: q [Sq, N, D], k/v [Sk, N, D] (unit d stride). ``exact``: running-max
+    softmax semantics (rows whose constant-max sum underflowed are recomputed, see attention_core)."""
     vt, _ = transpose_heads(v)
-    return attention_core(q, k, vt, head_max_norm(k), scale, out_mode)
+    return attention_core(q, k, vt, head_max_norm(k), scale, out_mode, exact=exact)
 
 
 def wan_cp_self_attention(query, key, value, scale, cp_size=1, cp_group=None, cp_replica_groups=None):
@@ -210,14 +224,15 @@ def wan_cp_self_attention(query, key, value, scale, cp_size=1, cp_group=None, cp
     ``[B, N, D, S]`` (the layout the o-projection consumes)."""
     if cp_size != 1:
         raise NotImplementedError("context-parallel attention spans several GPUs; this build runs on one")
-    outs = [_attend_bsnd(query[b], key[b], value[b], scale, OUT_DMAJOR) for b in range(query.shape[0])]
+    outs = [_attend_bsnd(query[b], key[b], value[b], scale, OUT_DMAJOR, True) for b in range(query.shape[0])]
     return torch.stack(outs, dim=0) if len(outs) > 1 else outs[0].unsqueeze(0)
 
 
 def _nki_attend(query, key, value, scale):
     """Non-causal attention over ``[B, N, S, D]`` q/k/v -> d-major ``[B, N, D, S_q]``."""
     outs = [
-        _attend_bsnd(query[b].transpose(0, 1), key[b].transpose(0, 1), value[b].transpose(0, 1), scale, OUT_DMAJOR)
+        _attend_bsnd(query[b].transpose(0, 1), key[b].transpose(0, 1), value[b].transpose(0, 1), scale, OUT_DMAJOR,
+                     True)
         for b in range(query.shape[0])
     ]
     return torch.stack(outs, dim=0) if len(outs) > 1 else outs[0].unsqueeze(0)
@@ -231,7 +246,7 @@ def attention_cte(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Te
     if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or q.shape[0] != k.shape[0] or k.shape != v.shape:
         raise ValueError(f"attention_cte expects [BN, S, 128] q/k/v, got {tuple(q.shape)}, {tuple(k.shape)}, "
                          f"{tuple(v.shape)}")
-    return _attend_bsnd(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), 1.0, OUT_DMAJOR)
+    return _attend_bsnd(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), 1.0, OUT_DMAJOR, True)
 
 
 def register_torch_ops() -> bool:
@@ -267,7 +282,7 @@ def ring_attention_const_max_fwd(q, k, v, replica_groups=None, num_workers=1, so
     scale = softmax_scale or 1.0 / math.sqrt(q.shape[-1])
     outs = []
     for b in range(q.shape[0]):
-        o = _attend_bsnd(q[b], k[b], v[b], scale, OUT_TOKEN)  # [S, h*d]
+        o = _attend_bsnd(q[b], k[b], v[b], scale, OUT_TOKEN, False)  # [S, h*d], the ring kernel's constant max
         outs.append(o.view(q.shape[1], q.shape[2], HEAD_DIM).transpose(0, 1))
     return torch.stack(outs, dim=0)
 

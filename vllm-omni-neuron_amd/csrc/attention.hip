@@ -65,6 +65,7 @@ struct AttnArgs {
   const float* q_sin;
   float q_eps;
   int heads_per_group;  // attention_head_group_kernel: consecutive heads per workgroup (divides heads)
+  float* row_sum;       // optional: each query's row sum of P, [heads][Sq] (wanmi_attention_exact)
 };
 
 // LDS tiles, a ring of kStages (tile t in slot t % kStages):
@@ -425,6 +426,7 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   const float inv = 1.0f / fmaxf(lsum, kSumFloor);
   const int64_t qi = q0 + col;
   const bool qok = qi < a.Sq;
+  if (a.row_sum != nullptr && qok && hq == 0) a.row_sum[(int64_t)h * a.Sq + qi] = lsum;
   if (a.out_mode == WANMI_ATTN_OUT_TOKEN) {
     uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi * a.o_ss;
 #pragma unroll
@@ -706,6 +708,7 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
     const float inv = 1.0f / fmaxf(lsum, kSumFloor);
     const int64_t qi = q0 + col;
     const bool qok = qi < a.Sq;
+    if (a.row_sum != nullptr && qok && hq == 0) a.row_sum[(int64_t)h * a.Sq + qi] = lsum;
     if (a.out_mode == WANMI_ATTN_OUT_TOKEN) {
       uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs + qi * o_ss;
 #pragma unroll
@@ -766,6 +769,108 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
         const int64_t qg = q0 + qr;
         if (qg < a.Sq) *reinterpret_cast<uint4*>(out + qg * o_ss + ch * 16) = v;
       }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Exact-softmax rescue for the constant-max kernels. The bound c_i = s ||q_i|| max_j ||k_j|| can
+// exceed the row's true largest logit by so much that every P = exp(s q_i.k_j - c_i) underflows and
+// the row sum collapses (c_i - max_j s q_i.k_j beyond about 87): the row then comes out as zero,
+// where a running-max flash attention (the reference's attention_cte) gives the softmax. While the
+// row sum is at least 2^-96 its largest P is at least 2^-113 for any Sk <= 2^17, a normal float, and
+// the P that flush to zero (each below 2^-126) carry less than 2^-13 of the sum: the row is
+// accurate. Rows below that (or NaN) are recomputed here, one wave per 64 rows of a head, each
+// flagged row in two passes over the keys in fp32: the true max m = max_j s q.k_j, then
+// sum_j exp(s q.k_j - m) v_j / sum_j exp(s q.k_j - m). V is read from V^T, whose 16-key groups hold
+// key (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1) in slot r (the order wanmi_transpose_heads writes,
+// an involution). Only the token-major and d-major bf16 outputs are rewritten.
+// ------------------------------------------------------------------------------------------------
+constexpr float kRescueSum = 0x1p-96f;
+
+__device__ __forceinline__ int vt_slot_key(int r) { return (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// s q.k_j for key j of head h: q (already scaled by s) in LDS as 128 floats
+__device__ __forceinline__ float rescue_logit(const AttnArgs& a, int h, int64_t j, const float* sq) {
+  const uint16_t* kp = a.k + h * a.k_hs + j * a.k_ss;
+  float dot = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const uint4 v = *reinterpret_cast<const uint4*>(kp + 8 * c);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      dot = fmaf(bf16_lo(w[t]), sq[8 * c + 2 * t], dot);
+      dot = fmaf(bf16_hi(w[t]), sq[8 * c + 2 * t + 1], dot);
+    }
+  }
+  return dot;
+}
+
+__global__ __launch_bounds__(64) void attention_rescue_kernel(AttnArgs a) {
+  __shared__ float sq[128];
+  __shared__ float sp[64];
+  const int lane = threadIdx.x;
+  const int h = blockIdx.y;
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  bool flag = false;
+  if (r0 + lane < a.Sq) {
+    const float rs = a.row_sum[(int64_t)h * a.Sq + r0 + lane];
+    flag = !(rs >= kRescueSum);
+  }
+  uint64_t pending = __ballot(flag);
+  while (pending) {
+    const int i = __builtin_ctzll(pending);
+    pending &= pending - 1;
+    const int64_t qi = r0 + i;
+    const uint32_t qw = *reinterpret_cast<const uint32_t*>(a.q + h * a.q_hs + qi * a.q_ss + 2 * lane);
+    __syncthreads();  // the previous row is done with sq and sp
+    sq[2 * lane] = bf16_lo(qw) * a.scale;
+    sq[2 * lane + 1] = bf16_hi(qw) * a.scale;
+    __syncthreads();
+    float m = -__builtin_inff();
+    for (int64_t j = lane; j < a.Sk; j += 64) m = fmaxf(m, rescue_logit(a, h, j, sq));
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float o0 = 0.0f, o1 = 0.0f, l = 0.0f;
+    const uint16_t* v0row = a.vt + ((int64_t)h * 128 + 2 * lane) * a.vt_ld;
+    const uint16_t* v1row = v0row + a.vt_ld;
+    for (int64_t j0 = 0; j0 < a.Sk; j0 += 64) {
+      const int64_t j = j0 + lane;
+      const float p = j < a.Sk ? __expf(rescue_logit(a, h, j, sq) - m) : 0.0f;
+      l += p;
+      __syncthreads();
+      sp[lane] = p;
+      __syncthreads();
+      // slots j0 .. j0 + 63 of this lane's two V^T rows (vt_ld is a multiple of 64 and >= Sk, so
+      // the chunk lies inside the row; keys past Sk have p = 0)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint4 x0 = *reinterpret_cast<const uint4*>(v0row + j0 + 8 * c);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(v1row + j0 + 8 * c);
+        const uint32_t w0[4] = {x0.x, x0.y, x0.z, x0.w}, w1[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int s0 = 8 * c + 2 * t;  // slot within the chunk
+          const float pa = sp[(s0 & ~15) | vt_slot_key(s0 & 15)];
+          const float pb = sp[((s0 + 1) & ~15) | vt_slot_key((s0 + 1) & 15)];
+          o0 = fmaf(pa, bf16_lo(w0[t]), o0);
+          o0 = fmaf(pb, bf16_hi(w0[t]), o0);
+          o1 = fmaf(pa, bf16_lo(w1[t]), o1);
+          o1 = fmaf(pb, bf16_hi(w1[t]), o1);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) l += __shfl_xor(l, o, 64);
+    const float inv = 1.0f / l;  // l >= 1: the max term is exp(0)
+    const uint32_t packed = pack_bf16x2(o0 * inv, o1 * inv);
+    uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + h * a.o_hs;
+    if (a.out_mode == WANMI_ATTN_OUT_TOKEN) {
+      *reinterpret_cast<uint32_t*>(out + qi * a.o_ss + 2 * lane) = packed;
+    } else {
+      out[qi + (2 * lane) * a.o_ds] = (uint16_t)(packed & 0xFFFFu);
+      out[qi + (2 * lane + 1) * a.o_ds] = (uint16_t)(packed >> 16);
     }
   }
 }
@@ -838,7 +943,7 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
                           const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
                           int out_mode, void* out, int64_t o_head_stride, int64_t o_token_stride,
                           int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride, const QPrep& qp,
-                          void* stream) {
+                          void* stream, float* row_sum = nullptr) {
   WANMI_REQUIRE(head_dim == 128, WANMI_ERR_UNSUPPORTED, "wanmi_attention_const_max: head_dim must be 128, got %d",
                 head_dim);
   WANMI_REQUIRE(Sq >= 0 && Sk > 0 && heads > 0 && heads <= 65535, WANMI_ERR_ARG,
@@ -893,6 +998,7 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
   a.q_cos = qp.cos;
   a.q_sin = qp.sin;
   a.q_eps = qp.eps;
+  a.row_sum = row_sum;
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
   const bool rebase_k = ((Sk - 1) * k_token_stride + 128) * 2 >= (1LL << 31);
   // Short key sequences of three tiles or more with queries that take no RoPE (cross-attention):
@@ -964,4 +1070,50 @@ extern "C" int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_str
   return attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq, Sk,
                         heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride, out_scales,
                         os_token_stride, qp, stream);
+}
+
+extern "C" int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64_t q_token_stride, const void* k,
+                                     int64_t k_head_stride, int64_t k_token_stride, const void* vt, int64_t vt_ld,
+                                     const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
+                                     int out_mode, void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                     int64_t o_d_stride, float* row_sum, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(out_mode == WANMI_ATTN_OUT_TOKEN || out_mode == WANMI_ATTN_OUT_DMAJOR, WANMI_ERR_ARG,
+                "wanmi_attention_exact: out_mode %d must be token-major or d-major bf16", out_mode);
+  WANMI_REQUIRE(row_sum && ((uintptr_t)row_sum % 4) == 0, WANMI_ERR_ARG,
+                "wanmi_attention_exact: row_sum must be a 4-byte aligned [heads][Sq] buffer");
+  WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_TOKEN || (((uintptr_t)out % 4) == 0 && o_head_stride % 2 == 0 &&
+                                                     o_token_stride % 2 == 0),
+                WANMI_ERR_ARG, "wanmi_attention_exact: token-major output rows must be 4-byte aligned");
+  WANMI_REQUIRE(vt_ld % 64 == 0 && ((uintptr_t)vt % 16) == 0 && ((uintptr_t)k % 16) == 0 &&
+                    k_token_stride % 8 == 0 && k_head_stride % 8 == 0 && ((uintptr_t)q % 4) == 0 &&
+                    q_token_stride % 2 == 0 && q_head_stride % 2 == 0,
+                WANMI_ERR_ARG, "wanmi_attention_exact: misaligned q/k/vt");
+  int st = attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq, Sk,
+                          heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride, nullptr, 0,
+                          QPrep{}, stream, row_sum);
+  if (st != WANMI_OK || Sq == 0) return st;
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_hs = q_head_stride;
+  a.q_ss = q_token_stride;
+  a.k = static_cast<const uint16_t*>(k);
+  a.k_hs = k_head_stride;
+  a.k_ss = k_token_stride;
+  a.vt = static_cast<const uint16_t*>(vt);
+  a.vt_ld = vt_ld;
+  a.Sq = Sq;
+  a.Sk = Sk;
+  a.heads = heads;
+  a.scale = scale;
+  a.out_mode = out_mode;
+  a.out = out;
+  a.o_hs = o_head_stride;
+  a.o_ss = o_token_stride;
+  a.o_ds = o_d_stride;
+  a.row_sum = row_sum;
+  hipLaunchKernelGGL(attention_rescue_kernel, dim3((unsigned)((Sq + 63) / 64), (unsigned)heads), dim3(64), 0,
+                     (hipStream_t)stream, a);
+  return check_launch("wanmi_attention_exact(rescue)");
 }
