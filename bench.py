@@ -4,8 +4,9 @@ Workload: 40 Wan2.2-A14B blocks (dim 5120, 40 heads x 128, FFN 13824), S = 32760
 (21x30x52 latent grid, 480x832x81 frames), 512 text tokens, MXFP8 projections and bf16 constant-max
 attention, one CFG branch, cross-attention K/V cached (projected once before timing, as the
 reference does per generation), the RoPE tables built inside every timed forward (as the reference
-builds them per forward). After the metric the same 40-block forward is measured at 720p
-(21x45x80 = 75600 tokens). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
+builds them per forward). After the metric the same 40 blocks are timed through the reference's own
+FP8 recipe (ROW activations, drop-ins composed as its modules call them; ``row_recipe``) and the
+40-block forward is measured at 720p (21x45x80 = 75600 tokens; ``p720``). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
 seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic data.
 
 Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). Per-kernel times
@@ -43,6 +44,7 @@ def parse():
     p.add_argument("--blocks", type=int, default=40)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-720p", action="store_true", help="skip the 720p (21x45x80) 40-block step timing")
+    p.add_argument("--no-row", action="store_true", help="skip the ROW-activation (reference recipe) step timing")
     p.add_argument("--pmc-calibration", action="store_true",
                    help="also run one 256 MiB device copy, the known-size reference for HBM counters")
     return p.parse_args()
@@ -193,6 +195,33 @@ def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
     }
 
 
+def row_recipe_step(pkg, row_blocks, row_crosses, tables, temb, h0, grid, steps=2, warmup=1):
+    """The reference's own FP8 recipe (ROW activations at every adaLN site, per-tensor FP8 weights
+    with per-channel scales, the drop-ins composed as its FP8 modules call them) over the same 40
+    blocks at the metric's length: `warmup` untimed forwards, then `steps` timed ones, with
+    per-step HIP events."""
+    rb = pkg.row_block
+    for _ in range(warmup):
+        rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, tables=tables)
+    timer = KernelTimer()
+    timer.active = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, timer=timer, tables=tables)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("non-finite ROW-recipe DiT output")
+    comp = {k: round(sum(v) / steps, 2) for k, v in sorted(timer.summary().items())}
+    return {
+        "workload": (f"the reference's FP8 block recipe (ROW activations, per-tensor FP8 weights with per-channel "
+                     f"scales, drop-ins composed as row_mx_modules.py calls them), {len(row_blocks)} blocks at "
+                     f"S={h0.shape[0]}"),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 1), "components_ms_per_step": comp,
+    }
+
+
 def copy_ceiling(traffic_bytes, adaln_gbs, reps=20):
     """Device-to-device copy moving the adaLN launch's bytes (half read, half written), timed with
     HIP events: the practical HBM rate of a streaming kernel on this box, beside the nominal 8 TB/s."""
@@ -228,7 +257,13 @@ def main():
     blk, ops = pkg.block, pkg.attention_ops
 
     gen = torch.Generator(device=dev).manual_seed(2024)
-    blocks = [blk.random_block_weights(dev, gen, qk_gamma_mean=1.0, keep_raw=False)[0] for _ in range(args.blocks)]
+    blocks, row_blocks = [], []
+    for _ in range(args.blocks):
+        w, raw = blk.random_block_weights(dev, gen, qk_gamma_mean=1.0, keep_raw=not args.no_row)
+        blocks.append(w)
+        if not args.no_row:  # the same weights as the checkpoint's per-tensor FP8 form
+            row_blocks.append(pkg.row_block.row_block_weights(raw)[0])
+        del raw
     h0 = torch.randn(S, DIM, device=dev, generator=gen).to(torch.bfloat16)
     temb = torch.randn(6, DIM, device=dev, generator=gen)
     ctx = torch.randn(TXT, DIM, device=dev, generator=gen).to(torch.bfloat16)
@@ -315,6 +350,10 @@ def main():
         },
     }
     result["hbm_copy_ceiling"] = copy_ceiling(plain, result["adaln_quant_gbs"])
+    if not args.no_row:
+        row_crosses = [pkg.row_block.project_cross_kv_row(w, ctx) for w in row_blocks]
+        result["row_recipe"] = row_recipe_step(pkg, row_blocks, row_crosses, tables, temb, h0, grid)
+        del row_blocks, row_crosses
     if not args.no_720p:
         result["p720"] = step_720p(pkg, blocks, crosses, tables, temb, dev)
     if not args.no_cpu_baseline:
