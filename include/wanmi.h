@@ -246,6 +246,23 @@ int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64_t q_token_
                           int64_t o_d_stride, float* row_sum, void* stream);
 
 /*
+ * wanmi_attention_exact without the row_sum workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * has no counterpart in the reference. The row sums live in a static device array of the library,
+ * 4M floats (16 MiB) on every GPU the library runs on, held until the process ends: heads * Sq
+ * must be at most 4194304 (WANMI_ERR_ARG otherwise). The array's device address is looked up once
+ * per device at the first call on it. Nothing is allocated or freed here. Every call on one GPU
+ * shares that GPU's array and leaves the last call's row sums in it, so calls that overlap on one
+ * GPU (different streams, or threads without ordering) race; calls in order on one stream do not.
+ * Arguments and results are those of wanmi_attention_exact.
+ */
+int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t q_token_stride, const void* k,
+                                  int64_t k_head_stride, int64_t k_token_stride, const void* vt, int64_t vt_ld,
+                                  const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
+                                  int out_mode, void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                  int64_t o_d_stride, void* stream);
+
+/*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,
  * hardware conversion; inputs must satisfy |x| < 464). Test hook for the conversion's known-answer
  * tests; it has no counterpart in the reference (which relies on torch's float8_e4m3fn cast,

@@ -131,7 +131,11 @@ def test_row_recipe_block(pkg, dev):
 
     def timer(name, fn):
         r = fn()
-        keep = tuple(x.clone() for x in r) if isinstance(r, tuple) else (r.clone() if isinstance(r, torch.Tensor) else r)
+        if isinstance(r, tuple):
+            parts = [x.clone() for x in r]
+            keep = type(r)(*parts) if hasattr(r, "_fields") else tuple(parts)
+        else:
+            keep = r.clone() if isinstance(r, torch.Tensor) else r
         snap.setdefault(name, []).append(keep)
         return r
 

@@ -48,6 +48,10 @@ _SIGNATURES = {
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _vp,
     ],
+    "wanmi_attention_exact_noalloc": [
+        _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
+        _vp, _i64, _i64, _i64, _vp,
+    ],
     "wanmi_attention_const_max_qprep": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _f32, _vp,

@@ -20,6 +20,8 @@
 // Q fragments the MFMA consumes.
 #include "wanmi_common.h"
 
+#include <mutex>
+
 namespace wanmi {
 
 constexpr int kAttnRsrcWord3 = 0x00020000;
@@ -1072,6 +1074,38 @@ extern "C" int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_str
                         os_token_stride, qp, stream);
 }
 
+namespace wanmi {
+// Row sums of the allocation-free exact attention (wanmi_attention_exact_noalloc): one fp32 per
+// (head, query), at most kNoAllocRowSums = 4M of them (16 MiB, held on every GPU the library runs
+// on until the process ends). In host code `scratch` names a host-side stand-in, not a device
+// address; the device copy's address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kNoAllocRowSums = int64_t(1) << 22;
+static __device__ __align__(256) float scratch[kNoAllocRowSums];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static float* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch`, looked up at the first call on the device (with it current).
+static int scratch_for_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  WANMI_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, WANMI_ERR_HIP,
+                "wanmi_attention_exact_noalloc: no current device (%s)", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    WANMI_REQUIRE(e == hipSuccess && ptr != nullptr, WANMI_ERR_HIP,
+                  "wanmi_attention_exact_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return WANMI_OK;
+}
+}  // namespace wanmi
+
 extern "C" int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64_t q_token_stride, const void* k,
                                      int64_t k_head_stride, int64_t k_token_stride, const void* vt, int64_t vt_ld,
                                      const float* kmax, int64_t Sq, int64_t Sk, int heads, int head_dim, float scale,
@@ -1116,4 +1150,23 @@ extern "C" int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64
   hipLaunchKernelGGL(attention_rescue_kernel, dim3((unsigned)((Sq + 63) / 64), (unsigned)heads), dim3(64), 0,
                      (hipStream_t)stream, a);
   return check_launch("wanmi_attention_exact(rescue)");
+}
+
+extern "C" int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                             const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                             const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq, int64_t Sk,
+                                             int heads, int head_dim, float scale, int out_mode, void* out,
+                                             int64_t o_head_stride, int64_t o_token_stride, int64_t o_d_stride,
+                                             void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(heads > 0 && Sq >= 0 && (int64_t)heads * Sq <= kNoAllocRowSums, WANMI_ERR_ARG,
+                "wanmi_attention_exact_noalloc: heads * Sq = %lld row sums exceed the %lld the library holds",
+                (long long)heads * (long long)Sq, (long long)kNoAllocRowSums);
+  float* row_sum = nullptr;
+  const int st = scratch_for_current_device(&row_sum);
+  if (st != WANMI_OK) return st;
+  return wanmi_attention_exact(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax,
+                               Sq, Sk, heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride,
+                               row_sum, stream);
 }
