@@ -263,6 +263,15 @@ int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t 
                                   int64_t o_d_stride, void* stream);
 
 /*
+ * Streaming device-to-device copy of `bytes` (a multiple of 16; src and dst 16-byte aligned, not
+ * overlapping) on `stream`: 16-byte loads, eight per thread in flight before its non-temporal
+ * stores, one 32 KiB chunk per workgroup. Measurement infrastructure with no counterpart in the
+ * reference: the practical HBM streaming rate the memory-bound kernels (adaLN + quantization, the
+ * K normalization pass) are compared against.
+ */
+int wanmi_hbm_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,
  * hardware conversion; inputs must satisfy |x| < 464). Test hook for the conversion's known-answer
  * tests; it has no counterpart in the reference (which relies on torch's float8_e4m3fn cast,

@@ -52,6 +52,7 @@ _SIGNATURES = {
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp,
     ],
+    "wanmi_hbm_stream_copy": [_vp, _vp, _i64, _vp],
     "wanmi_attention_const_max_qprep": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _f32, _vp,
@@ -87,6 +88,22 @@ def load() -> ctypes.CDLL:
 
 def exported_symbols() -> list[str]:
     return list(_SIGNATURES)
+
+
+def hbm_stream_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """Copy ``src`` into ``dst`` (same number of bytes, a multiple of 16; contiguous, on one GPU)
+    with the library's streaming copy kernel, on the current stream. Measurement helper: the
+    practical HBM streaming rate the memory-bound kernels are compared against."""
+    lib = load()
+    if src.device.type != "cuda" or dst.device != src.device:
+        raise RuntimeError("hbm_stream_copy: src and dst must be on the same GPU; no CPU fallback")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("hbm_stream_copy: src and dst must be contiguous")
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != n:
+        raise ValueError("hbm_stream_copy: src and dst must hold the same number of bytes")
+    check(lib.wanmi_hbm_stream_copy(ptr(src), ptr(dst), n, stream_of(src)), "wanmi_hbm_stream_copy")
+    return dst
 
 
 def check(status: int, what: str) -> None:
