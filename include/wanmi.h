@@ -144,6 +144,19 @@ int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float
                           const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
                           float* maxnorm, void* stream);
 
+/*
+ * wanmi_qk_rmsnorm_rope that also writes the queries' across-heads 1/rms for the attention's fused Q
+ * preparation: q_rr[t] = 1 / sqrt(sum_b q_sumsq[t * q_sumsq_ld + b] / (q_heads * 128) + q_eps), the
+ * sum taken in fp32 over the blocks b = 0 .. q_heads-1 in order and the root in fp64 (exactly what
+ * wanmi_attention_const_max_qprep computes from the same partials). The K pass runs between the QKV
+ * projection and the attention anyway; computed here once per token, the 1/rms costs the attention
+ * one load per query (wanmi_attention_const_max_qrr) instead of q_heads per head. Replaces the same
+ * reference interfaces as wanmi_qk_rmsnorm_rope.
+ */
+int wanmi_qk_rmsnorm_rope_qrr(void* x, int64_t S, int64_t ld, int heads, const float* gamma, const float* cos_tab,
+                              const float* sin_tab, int rope_pairs, float eps, float* maxnorm, const float* q_sumsq,
+                              int64_t q_sumsq_ld, int q_heads, float q_eps, float* q_rr, void* stream);
+
 /* Table layouts of wanmi_rope_tables (per token s, fp32). */
 #define WANMI_ROPE_PAIRS 0       /* [S, head_dim/2]: angle i of pair i (the kernels' own tables) */
 #define WANMI_ROPE_INTERLEAVED 1 /* [S, head_dim]: each angle twice, (c0, c0, c1, c1, ...) -- the
@@ -225,6 +238,22 @@ int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_stride, int64_
                                     int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
                                     const float* q_sumsq, int64_t q_sumsq_ld, const float* q_gamma,
                                     const float* q_cos, const float* q_sin, float q_eps, void* stream);
+
+/*
+ * wanmi_attention_const_max_qprep with each query's across-heads 1/rms given, q_rr [Sq] fp32, in place
+ * of the partial sums (as wanmi_qk_rmsnorm_rope_qrr computes it from them: the same operations in the
+ * same order, so the result is bit-identical to passing the partials). The Q load then reads one
+ * float per query instead of `heads` partial sums for every head. Replaces the same reference
+ * interfaces as wanmi_attention_const_max_qprep.
+ */
+int wanmi_attention_const_max_qrr(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                  const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                  const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                  int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                  void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                  int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                  const float* q_rr, const float* q_gamma, const float* q_cos,
+                                  const float* q_sin, void* stream);
 
 /*
  * Exact-softmax attention for the drop-ins of a running-max flash attention: the reference's

@@ -304,3 +304,46 @@ def test_exact_dropins_survive_a_loose_bound(pkg, dev, Sk):
     o3 = torch.ops.wan_transformer.attention_cte(qs.to(dev), kb.to(dev), vb.to(dev)).cpu()
     ref3 = oa.torch_attend(qs[None], kb[None], vb[None], 1.0, dtype=torch.float64)[0]
     _check_attn(o3.transpose(1, 2), ref3)
+
+
+@pytest.mark.parametrize("Sk,with_rope", [(1900, True), (512, False), (200, True)])
+def test_query_rrms_from_the_k_pass_is_bit_identical(pkg, dev, Sk, with_rope):
+    """The K pass's per-token Q 1/rms (``qk_rmsnorm_rope_(..., q_sumsq=, q_rr=)``) equals, bit for
+    bit, the fp32 block-ordered sum of the partials with the root in fp64 (restated here on the
+    CPU), and the attention reading it (``QPrep(rr=...)``) gives the same bits as the attention
+    summing the partials itself -- the one-head kernel with RoPE (1900 keys), the head-group kernel
+    without (512 keys, 40 heads), the short-key kernel (200 keys) -- in MX and token-major output.
+    Sq = 1000 leaves a ragged last query block; partials with a stride wider than the heads."""
+    ops = pkg.attention_ops
+    Sq, N, grid = 1000, 40, (1, 20, 50)
+    g = torch.Generator().manual_seed(Sk)
+    q = torch.randn(Sq, N * 128, generator=g).to(torch.bfloat16)
+    kslab = torch.randn(Sq, N * 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(N * 128, generator=g)).float()
+    ss = torch.zeros(Sq, 2 * N)
+    ss[:, :N] = q.float().pow(2).view(Sq, N, 128).sum(-1) * (1 + 0.01 * torch.rand(Sq, N, generator=g))
+    cos, sin = orope.wan_rope(grid)
+    c64, s64 = ops.rope_pair_tables(cos.to(dev), sin.to(dev))
+    c64, s64 = (c64, s64) if with_rope else (None, None)
+    ssd = ss.to(dev)
+    rr = torch.full((Sq,), float("nan"), device=dev)
+    ops.qk_rmsnorm_rope_(kslab.to(dev), gamma.to(dev), cos=c64, sin=s64, eps=1e-6, q_sumsq=ssd, q_rr=rr)
+    # the restatement: sequential fp32 sum over the 40 blocks, fp64 root
+    acc = np.zeros(Sq, np.float32)
+    for b in range(N):
+        acc = (acc + ss[:, b].numpy()).astype(np.float32)
+    want = (1.0 / np.sqrt((acc / np.float32(N * 128)).astype(np.float64) + np.float64(np.float32(1e-6)))).astype(np.float32)
+    np.testing.assert_array_equal(rr.cpu().numpy(), want)
+    qd, kd = q.to(dev).view(Sq, N, 128), k.to(dev)
+    vt, _ = ops.transpose_heads(v.to(dev))
+    kmax = ops.head_max_norm(kd)
+    for mode in (ops.OUT_MX, ops.OUT_TOKEN):
+        a = ops.attention_core(qd, kd, vt, kmax, 128**-0.5, mode, q_prep=ops.QPrep(ssd, gamma.to(dev), c64, s64, 1e-6))
+        b = ops.attention_core(qd, kd, vt, kmax, 128**-0.5, mode, q_prep=ops.QPrep(None, gamma.to(dev), c64, s64,
+                                                                                  rr=rr))
+        if mode == ops.OUT_MX:
+            assert torch.equal(a.codes.view(torch.uint8), b.codes.view(torch.uint8)) and torch.equal(a.scales, b.scales)
+        else:
+            assert torch.equal(a, b)

@@ -53,6 +53,11 @@ _SIGNATURES = {
         _vp, _i64, _i64, _i64, _vp,
     ],
     "wanmi_hbm_stream_copy": [_vp, _vp, _i64, _vp],
+    "wanmi_qk_rmsnorm_rope_qrr": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
+    "wanmi_attention_const_max_qrr": [
+        _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
+        _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+    ],
     "wanmi_attention_const_max_qprep": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
         _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _f32, _vp,

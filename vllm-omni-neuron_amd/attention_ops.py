@@ -59,12 +59,17 @@ def _check_rope_tables(cos, sin, S: int, what: str) -> None:
 
 
 def qk_rmsnorm_rope_(x: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None, eps: float = 1e-6,
-                     want_max: bool = False, rope_pairs: str = "interleaved"):
+                     want_max: bool = False, rope_pairs: str = "interleaved", q_sumsq: torch.Tensor | None = None,
+                     q_rr: torch.Tensor | None = None, q_eps: float | None = None):
     """In place on a bf16 ``[S, heads*128]`` view (unit column stride): across-heads RMSNorm * gamma,
     then RoPE with pair tables ``cos``/``sin`` fp32 ``[S, 64]`` when given, on the channel pairs
     ``rope_pairs`` names (``"interleaved"``: (2i, 2i+1); ``"halves"``: (i, i+64), the rotate-half
     order of de-interleaved channels). Returns the per-head max norm ``[heads]`` (fp32) when
-    ``want_max``."""
+    ``want_max``.
+
+    ``q_sumsq`` (fp32 ``[S, >= heads]``, the QKV GEMM's per-128-column partial sums of squares of Q)
+    with ``q_rr`` (fp32 ``[S]``, written): also the queries' across-heads 1/rms, for the attention's
+    fused Q preparation (``QPrep(rr=q_rr)``), with ``q_eps`` (default ``eps``)."""
     lib = _lib.load()
     if rope_pairs not in _ROTATE:
         raise ValueError(f"unknown rope_pairs {rope_pairs!r}")
@@ -82,6 +87,21 @@ def qk_rmsnorm_rope_(x: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None
     _lib.require_gpu(x, gamma, cos, sin, what="qk_rmsnorm_rope")
     gamma = gamma.reshape(W).to(torch.float32).contiguous()
     kmax = torch.empty(heads, dtype=torch.float32, device=x.device) if want_max else None
+    if (q_sumsq is None) != (q_rr is None):
+        raise ValueError("q_sumsq and q_rr go together")
+    if q_rr is not None:
+        _lib.expect(q_sumsq, "q_sumsq", dtype=torch.float32, shape=(S, None), contiguous=False, row_contiguous=True)
+        if q_sumsq.shape[1] < heads:
+            raise ValueError(f"q_sumsq needs at least {heads} partial sums per row")
+        _lib.expect(q_rr, "q_rr", dtype=torch.float32, shape=(S,))
+        _lib.require_gpu(q_sumsq, q_rr, x, what="qk_rmsnorm_rope")
+        st = lib.wanmi_qk_rmsnorm_rope_qrr(
+            _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), _ROTATE[rope_pairs],
+            float(eps), _lib.ptr(kmax), _lib.ptr(q_sumsq), q_sumsq.stride(0), heads,
+            float(eps if q_eps is None else q_eps), _lib.ptr(q_rr), _lib.stream_of(x),
+        )
+        _lib.check(st, "wanmi_qk_rmsnorm_rope_qrr")
+        return kmax
     st = lib.wanmi_qk_rmsnorm_rope(
         _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), _ROTATE[rope_pairs],
         float(eps), _lib.ptr(kmax), _lib.stream_of(x),
@@ -120,13 +140,16 @@ class QPrep(NamedTuple):
     """Q preparation fused into the attention's Q load: ``sumsq`` fp32 ``[Sq, >= N]`` per-128-column
     partial sums of squares of the raw q rows (from ``mxfp8_linear(..., row_sumsq=...)``), ``gamma``
     fp32 ``[N*128]`` (the across-heads RMSNorm weight), optional RoPE pair tables ``cos``/``sin``
-    fp32 ``[Sq, 64]``, and the norm's ``eps``."""
+    fp32 ``[Sq, 64]``, and the norm's ``eps``. ``rr`` (fp32 ``[Sq]``): each query's 1/rms already
+    computed from those partials (``qk_rmsnorm_rope_(..., q_sumsq=, q_rr=)``); given, ``sumsq`` and
+    ``eps`` are not used and the Q load reads one float per query."""
 
-    sumsq: torch.Tensor
+    sumsq: torch.Tensor | None
     gamma: torch.Tensor
     cos: torch.Tensor | None = None
     sin: torch.Tensor | None = None
     eps: float = 1e-6
+    rr: torch.Tensor | None = None
 
 
 def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: torch.Tensor, scale: float,
@@ -166,14 +189,17 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
     if out_mode not in (OUT_TOKEN, OUT_DMAJOR, OUT_MX):
         raise ValueError(f"unknown out_mode {out_mode}")
     if q_prep is not None:
-        _lib.expect(q_prep.sumsq, "q_prep.sumsq", dtype=torch.float32, shape=(Sq, None), contiguous=False,
-                    row_contiguous=True)
-        if q_prep.sumsq.shape[1] < N:
-            raise ValueError(f"q_prep.sumsq needs at least {N} partial sums per row")
+        if q_prep.rr is not None:
+            _lib.expect(q_prep.rr, "q_prep.rr", dtype=torch.float32, shape=(Sq,))
+        else:
+            _lib.expect(q_prep.sumsq, "q_prep.sumsq", dtype=torch.float32, shape=(Sq, None), contiguous=False,
+                        row_contiguous=True)
+            if q_prep.sumsq.shape[1] < N:
+                raise ValueError(f"q_prep.sumsq needs at least {N} partial sums per row")
         if not isinstance(q_prep.gamma, torch.Tensor) or q_prep.gamma.numel() != N * D:
             raise ValueError(f"q_prep.gamma must hold {N * D} elements")
         _check_rope_tables(q_prep.cos, q_prep.sin, Sq, "attention q_prep")
-        _lib.require_gpu(q_prep.sumsq, q_prep.gamma, q_prep.cos, q_prep.sin, what="attention")
+        _lib.require_gpu(q_prep.sumsq, q_prep.rr, q_prep.gamma, q_prep.cos, q_prep.sin, what="attention")
     _lib.require_gpu(q, k, vt, kmax, out, what="attention")
     dev = q.device
     scales = None
@@ -199,6 +225,13 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, kmax: tor
     elif q_prep is None:
         st = lib.wanmi_attention_const_max(*common, _lib.stream_of(q))
         _lib.check(st, "wanmi_attention_const_max")
+    elif q_prep.rr is not None:
+        gamma = q_prep.gamma.reshape(-1).to(torch.float32).contiguous()
+        st = lib.wanmi_attention_const_max_qrr(
+            *common, _lib.ptr(q_prep.rr), _lib.ptr(gamma), _lib.ptr(q_prep.cos), _lib.ptr(q_prep.sin),
+            _lib.stream_of(q),
+        )
+        _lib.check(st, "wanmi_attention_const_max_qrr")
     else:
         ss = q_prep.sumsq
         gamma = q_prep.gamma.reshape(-1).to(torch.float32).contiguous()

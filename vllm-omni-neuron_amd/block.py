@@ -151,11 +151,14 @@ def block_forward(w: BlockWeights, h: torch.Tensor, temb: torch.Tensor, rope, cr
     # before the attention starts.
     q_ss = torch.empty((S, 2 * dim // 128), dtype=torch.float32, device=h.device)
     qk, vt = run("gemm_qkv", lambda: mxfp8_qkv_linear(a1, w.qkv, vt_col0=2 * dim, row_sumsq=q_ss, sumsq_cols=dim))
-    kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qk[:, dim:], w.norm_k, cos=cos, sin=sin, eps=eps, want_max=True))
+    # the K pass also reduces each query's partial sums to its 1/rms, once per token
+    q_rr = torch.empty(S, dtype=torch.float32, device=h.device)
+    kmax = run("qk_prep", lambda: ops.qk_rmsnorm_rope_(qk[:, dim:], w.norm_k, cos=cos, sin=sin, eps=eps, want_max=True,
+                                                        q_sumsq=q_ss, q_rr=q_rr))
     q = qk[:, :dim].view(S, heads, HEAD_DIM)
     k = qk[:, dim:].view(S, heads, HEAD_DIM)
     o1 = run("self_attention", lambda: ops.attention_core(q, k, vt, kmax, scale, ops.OUT_MX,
-                                                         q_prep=ops.QPrep(q_ss, w.norm_q, cos, sin, eps)))
+                                                         q_prep=ops.QPrep(None, w.norm_q, cos, sin, eps, rr=q_rr)))
     h1 = run("gemm_o", lambda: mxfp8_linear(o1, w.o, epilogue="gated_residual", residual=h, gate=gate))
     a2 = run("adaln", lambda: adaln_quant_2d(h1, w.norm2_weight, w.norm2_bias, eps=eps, norm_type="layer_norm",
                                              quant="mx"))

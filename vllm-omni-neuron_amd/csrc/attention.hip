@@ -68,6 +68,7 @@ struct AttnArgs {
   float q_eps;
   int heads_per_group;  // attention_head_group_kernel: consecutive heads per workgroup (divides heads)
   float* row_sum;       // optional: each query's row sum of P, [heads][Sq] (wanmi_attention_exact)
+  const float* q_rr;    // optional (with q_gamma): each query's across-heads 1/rms [Sq], in place of q_sumsq
 };
 
 // LDS tiles, a ring of kStages (tile t in slot t % kStages):
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
   // Every load of the prologue (Q, gamma, cos/sin, the partial sums) is issued before any of them is
   // used: issued per fragment and used at once, the loads were eight dependent memory round trips
   // (about 9 us per workgroup, 40% of a cross-attention launch).
-  const bool qprep = a.q_sumsq != nullptr;
+  const bool qprep = a.q_sumsq != nullptr || a.q_rr != nullptr;
   const bool qrope = qprep && a.q_cos != nullptr;
   // The head's gamma (128 floats, the same for every query) goes to LDS, one copy per wave so that no
   // barrier is needed before the wave reads it; read per lane from L2 it was 16 loads of 1 KiB per
@@ -283,6 +284,13 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
 #pragma unroll
       for (int t = 0; t < 8; ++t) cv[t] = sv[t] = u32x4{0u, 0u, 0u, 0u};
     }
+    float rr;
+    if (a.q_rr != nullptr) {
+      // the query's 1/rms, computed once per token by the K pass from the same partials, in the same
+      // order, as the branch below (rows past Sq read as zero)
+      const __amdgpu_buffer_rsrc_t r_rr = attn_rsrc(a.q_rr + (qvalid > 0 ? q0 : 0), qvalid * 4);
+      rr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_rr, (uint32_t)col * 4, 0, 0));
+    } else {
     const __amdgpu_buffer_rsrc_t r_ss = attn_rsrc(a.q_sumsq + (qvalid > 0 ? q0 * a.qss_ld : 0),
                                                   qvalid > 0 ? ((qvalid - 1) * a.qss_ld + a.heads) * 4 : 0);
     float ss = 0.0f;
@@ -317,7 +325,8 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
         for (int j = 0; j < 4; ++j) ss = ss + __uint_as_float(v[j]);
       }
     }
-    const float rr = (float)(1.0 / sqrt((double)(ss / (float)(a.heads * 128)) + (double)a.q_eps));
+    rr = (float)(1.0 / sqrt((double)(ss / (float)(a.heads * 128)) + (double)a.q_eps));
+    }
     // every load of the prologue is in (the math below needs them all), the gamma copy included
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     const float4* gl = reinterpret_cast<const float4*>(sgam[wave]);
@@ -567,7 +576,7 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
     for (int t = 0; t < 8; ++t)
       qv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
   };
-  const bool qprep = a.q_sumsq != nullptr;
+  const bool qprep = a.q_sumsq != nullptr || a.q_rr != nullptr;
   auto issue_gamma = [&](int hd) {
     if (qprep) lds_dma_b128(buffer_rsrc(a.q_gamma + hd * 128, 128 * 4), (uint32_t)lane * 16, lds_addr(sgam[wave]));
   };
@@ -577,7 +586,10 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
   // the queries' across-heads 1/rms, from the partial sums in block order (as in
   // attention_const_max_kernel: lane halves read twenty blocks each and swap)
   float rr = 0.0f;
-  if (qprep) {
+  if (qprep && a.q_rr != nullptr) {
+    const __amdgpu_buffer_rsrc_t r_rr = attn_rsrc(a.q_rr + (qvalid > 0 ? q0 : 0), qvalid * 4);
+    rr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_rr, (uint32_t)col * 4, 0, 0));
+  } else if (qprep) {
     const __amdgpu_buffer_rsrc_t r_ss = attn_rsrc(a.q_sumsq + (qvalid > 0 ? q0 * a.qss_ld : 0),
                                                   qvalid > 0 ? ((qvalid - 1) * a.qss_ld + a.heads) * 4 : 0);
     float ss = 0.0f;
@@ -932,6 +944,7 @@ extern "C" int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t t
 
 namespace wanmi {
 struct QPrep {
+  const float* rr = nullptr;  // per-query 1/rms (in place of sumsq)
   const float* sumsq = nullptr;
   int64_t ld = 0;
   const float* gamma = nullptr;
@@ -995,6 +1008,7 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
   a.out_scales = out_scales;
   a.os_ss = os_token_stride;
   a.q_sumsq = qp.sumsq;
+  a.q_rr = qp.rr;
   a.qss_ld = qp.ld;
   a.q_gamma = qp.gamma;
   a.q_cos = qp.cos;
@@ -1038,6 +1052,32 @@ extern "C" int wanmi_attention_const_max(const void* q, int64_t q_head_stride, i
   return wanmi::attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq,
                                Sk, heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride,
                                out_scales, os_token_stride, wanmi::QPrep{}, stream);
+}
+
+extern "C" int wanmi_attention_const_max_qrr(const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                             const void* k, int64_t k_head_stride, int64_t k_token_stride,
+                                             const void* vt, int64_t vt_ld, const float* kmax, int64_t Sq,
+                                             int64_t Sk, int heads, int head_dim, float scale, int out_mode,
+                                             void* out, int64_t o_head_stride, int64_t o_token_stride,
+                                             int64_t o_d_stride, uint8_t* out_scales, int64_t os_token_stride,
+                                             const float* q_rr, const float* q_gamma, const float* q_cos,
+                                             const float* q_sin, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(q_rr && q_gamma, WANMI_ERR_ARG, "wanmi_attention_const_max_qrr: q_rr and q_gamma are required");
+  WANMI_REQUIRE((q_cos == nullptr) == (q_sin == nullptr), WANMI_ERR_ARG,
+                "wanmi_attention_const_max_qrr: q_cos and q_sin must both be given or both be null");
+  WANMI_REQUIRE(((uintptr_t)q_rr % 4) == 0 && ((uintptr_t)q_gamma % 16) == 0 &&
+                    (!q_cos || (((uintptr_t)q_cos % 16) == 0 && ((uintptr_t)q_sin % 16) == 0)),
+                WANMI_ERR_ARG, "wanmi_attention_const_max_qrr: q_rr must be 4-byte, q_gamma, q_cos, q_sin 16-byte aligned");
+  QPrep qp;
+  qp.rr = q_rr;
+  qp.gamma = q_gamma;
+  qp.cos = q_cos;
+  qp.sin = q_sin;
+  return attention_impl(q, q_head_stride, q_token_stride, k, k_head_stride, k_token_stride, vt, vt_ld, kmax, Sq, Sk,
+                        heads, head_dim, scale, out_mode, out, o_head_stride, o_token_stride, o_d_stride, out_scales,
+                        os_token_stride, qp, stream);
 }
 
 extern "C" int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_stride, int64_t q_token_stride,

@@ -37,6 +37,13 @@ struct QKNormArgs {
   const float* sin;  // [S, 64]
   float eps;
   float* maxnorm;  // [heads] or null (must be zeroed first)
+  // optional: the queries' across-heads 1/rms from the QKV GEMM's per-128-column partial sums of
+  // squares q_sumsq [S, qss_ld] (blocks 0 .. q_heads-1 in order), written to q_rr [S]
+  const float* q_sumsq;
+  int64_t qss_ld;
+  int q_heads;
+  float q_eps;
+  float* q_rr;
 };
 
 
@@ -72,6 +79,19 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
   float kmx[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) kmx[c] = 0.0f;
+
+  if (a.q_rr != nullptr) {
+    // lane i < tokens_per_wave: the Q 1/rms of token t0 + i, its partial sums added in block order
+    // and the root taken in fp64 -- the operations, in the order, the attention's Q load performs on
+    // the same partials (so the attention may read this instead, bit for bit)
+    const int64_t tq = t0 + lane;
+    if (lane < a.tokens_per_wave && tq < a.S) {
+      const float* pq = a.q_sumsq + tq * a.qss_ld;
+      float qs = 0.0f;
+      for (int b = 0; b < a.q_heads; ++b) qs = qs + pq[b];
+      a.q_rr[tq] = (float)(1.0 / sqrt((double)(qs / (float)(a.q_heads * 128)) + (double)a.q_eps));
+    }
+  }
 
   for (int it = 0; it < a.tokens_per_wave; ++it) {
     const int64_t t = t0 + it;
@@ -269,11 +289,10 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(TransposeArgs a) {
 
 }  // namespace wanmi
 
-extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
-                                     const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
-                                     float* maxnorm, void* stream) {
-  using namespace wanmi;
-  clear_error();
+namespace wanmi {
+static int qk_rmsnorm_rope_impl(void* x, int64_t S, int64_t ld, int heads, const float* gamma, const float* cos_tab,
+                                const float* sin_tab, int rope_pairs, float eps, float* maxnorm, const float* q_sumsq,
+                                int64_t q_sumsq_ld, int q_heads, float q_eps, float* q_rr, void* stream) {
   WANMI_REQUIRE(S >= 0 && heads > 0 && heads % 4 == 0 && heads <= 128, WANMI_ERR_ARG,
                 "wanmi_qk_rmsnorm_rope: need S >= 0 and heads a positive multiple of 4 (<= 128), got S=%lld heads=%d",
                 (long long)S, heads);
@@ -306,6 +325,11 @@ extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, 
   a.sin = sin_tab;
   a.eps = eps;
   a.maxnorm = maxnorm;
+  a.q_sumsq = q_sumsq;
+  a.qss_ld = q_sumsq_ld;
+  a.q_heads = q_heads;
+  a.q_eps = q_eps;
+  a.q_rr = q_rr;
   const int64_t waves = (S + a.tokens_per_wave - 1) / a.tokens_per_wave;
   const dim3 grid((unsigned)((waves + 3) / 4));
   if (rope_pairs == WANMI_ROTATE_HALVES) {
@@ -320,6 +344,31 @@ extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, 
     else hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<32, false>), grid, dim3(256), 0, s, a);
   }
   return check_launch("wanmi_qk_rmsnorm_rope");
+}
+}  // namespace wanmi
+
+extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
+                                     const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
+                                     float* maxnorm, void* stream) {
+  wanmi::clear_error();
+  return wanmi::qk_rmsnorm_rope_impl(x, S, ld, heads, gamma, cos_tab, sin_tab, rope_pairs, eps, maxnorm, nullptr, 0, 0,
+                                     0.0f, nullptr, stream);
+}
+
+extern "C" int wanmi_qk_rmsnorm_rope_qrr(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
+                                         const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
+                                         float* maxnorm, const float* q_sumsq, int64_t q_sumsq_ld, int q_heads,
+                                         float q_eps, float* q_rr, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(q_sumsq && q_rr && ((uintptr_t)q_sumsq % 4) == 0 && ((uintptr_t)q_rr % 4) == 0, WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope_qrr: q_sumsq and q_rr must be 4-byte aligned pointers");
+  WANMI_REQUIRE(q_heads > 0 && q_sumsq_ld >= q_heads, WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope_qrr: need q_heads > 0 and q_sumsq_ld >= q_heads (q_heads=%d, ld=%lld)", q_heads,
+                (long long)q_sumsq_ld);
+  WANMI_REQUIRE(!(q_eps < 0.0f), WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope_qrr: q_eps must be >= 0");
+  return qk_rmsnorm_rope_impl(x, S, ld, heads, gamma, cos_tab, sin_tab, rope_pairs, eps, maxnorm, q_sumsq, q_sumsq_ld,
+                              q_heads, q_eps, q_rr, stream);
 }
 
 extern "C" int wanmi_transpose_heads(const void* v, int64_t S, int64_t ld, int64_t head_stride, int heads,
