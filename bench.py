@@ -225,8 +225,9 @@ def row_recipe_step(pkg, row_blocks, row_crosses, tables, temb, h0, grid, steps=
 def copy_ceiling(pkg, traffic_bytes, adaln_gbs, reps=20):
     """The practical HBM streaming rate on this box, beside the nominal 8 TB/s: a copy moving the
     adaLN launch's bytes (half read, half written) through the library's streaming copy kernel
-    (16-byte loads, eight per thread in flight, non-temporal stores), and through torch's generic
-    device copy for comparison, each timed with HIP events over `reps` copies."""
+    (16-byte loads, eight per thread in flight, non-temporal stores) and through torch's generic
+    device copy for comparison, and the library's read-2-write-1 pass over the same bytes (the
+    adaLN pass's own mix), each timed with HIP events over `reps` launches."""
     n = traffic_bytes // 2 // 16 * 16
     src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
@@ -248,8 +249,17 @@ def copy_ceiling(pkg, traffic_bytes, adaln_gbs, reps=20):
         raise RuntimeError("streaming copy mismatch")
     ms_t, gbs_t = rate(lambda: dst.copy_(src))
     del src, dst
+    # the adaLN pass's own mix: two bytes read per byte written (bf16 in, e4m3 out)
+    nf = traffic_bytes * 2 // 3 // 32768 * 32768
+    src = torch.empty(nf, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty(nf // 2, dtype=torch.uint8, device="cuda")
+    ms_f, _ = rate(lambda: pkg._lib.hbm_stream_fold(dst, src))
+    gbs_f = (nf + nf // 2) / ms_f / 1e6
+    del src, dst
     return {"bytes_per_copy": 2 * n, "ms_per_copy": round(ms_k, 4), "gbs": round(gbs_k, 1),
-            "adaln_frac_of_copy": round(adaln_gbs / gbs_k, 3), "torch_copy_gbs": round(gbs_t, 1)}
+            "adaln_frac_of_copy": round(adaln_gbs / gbs_k, 3), "torch_copy_gbs": round(gbs_t, 1),
+            "read2_write1_bytes": nf + nf // 2, "read2_write1_gbs": round(gbs_f, 1),
+            "adaln_frac_of_read2_write1": round(adaln_gbs / gbs_f, 3)}
 
 
 def main():

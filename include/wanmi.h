@@ -301,6 +301,16 @@ int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t 
 int wanmi_hbm_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /*
+ * Streaming read-2-write-1 pass (measurement infrastructure, no counterpart in the reference):
+ * reads `src_bytes` (a multiple of 32768) and writes src_bytes / 2 to dst. Chunk k of 32 KiB is
+ * read as 2048 16-byte words w[0..2047] in the order thread t of 256 reads w[256 i + t], i < 8;
+ * output chunk k (16 KiB) holds, in 16-byte slot 256 i + t (i < 4), w[256 (2 i) + t] xor
+ * w[256 (2 i + 1) + t]. Same load and store form as the copy; its rate is the HBM ceiling for the
+ * adaLN + MX pass's 2:1 read/write mix.
+ */
+int wanmi_hbm_stream_fold(const void* src, void* dst, int64_t src_bytes, void* stream);
+
+/*
  * Element-wise fp32 -> e4m3fn conversion exactly as the kernels perform it (round to nearest even,
  * hardware conversion; inputs must satisfy |x| < 464). Test hook for the conversion's known-answer
  * tests; it has no counterpart in the reference (which relies on torch's float8_e4m3fn cast,

@@ -22,3 +22,25 @@ def test_stream_copy_rejects_ragged_sizes(pkg, dev):
     src = torch.zeros(24, dtype=torch.uint8, device=dev)
     with pytest.raises(ValueError, match="multiple of 16"):
         pkg._lib.hbm_stream_copy(torch.zeros_like(src), src)
+
+
+@pytest.mark.parametrize("chunks", [1, 3, 257])
+def test_stream_fold_xors_the_word_pairs(pkg, dev, chunks):
+    """The read-2-write-1 pass: output slot 256 i + t of chunk k is word 256 (2 i) + t xor word
+    256 (2 i + 1) + t of the chunk's 2048 16-byte words."""
+    n = chunks * 32768
+    g = torch.Generator(device=dev).manual_seed(chunks)
+    src = torch.randint(-2**31, 2**31 - 1, (n // 4,), dtype=torch.int32, device=dev, generator=g)
+    dst = torch.zeros(n // 8 + 16, dtype=torch.int32, device=dev)
+    pkg._lib.hbm_stream_fold(dst[: n // 8], src)
+    torch.cuda.synchronize()
+    w = src.view(chunks, 4, 2, 256, 4)  # [chunk, i, pair, t, word]
+    ref = (w[:, :, 0] ^ w[:, :, 1]).reshape(-1)
+    assert torch.equal(dst[: n // 8], ref)
+    assert not bool(dst[n // 8:].any())
+
+
+def test_stream_fold_rejects_partial_chunks(pkg, dev):
+    src = torch.zeros(32768 + 16, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError, match="multiple of 32768"):
+        pkg._lib.hbm_stream_fold(torch.zeros(src.numel() // 2, dtype=torch.uint8, device=dev), src)

@@ -53,6 +53,7 @@ _SIGNATURES = {
         _vp, _i64, _i64, _i64, _vp,
     ],
     "wanmi_hbm_stream_copy": [_vp, _vp, _i64, _vp],
+    "wanmi_hbm_stream_fold": [_vp, _vp, _i64, _vp],
     "wanmi_qk_rmsnorm_rope_qrr": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
     "wanmi_attention_const_max_qrr": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,
@@ -108,6 +109,25 @@ def hbm_stream_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
     if dst.numel() * dst.element_size() != n:
         raise ValueError("hbm_stream_copy: src and dst must hold the same number of bytes")
     check(lib.wanmi_hbm_stream_copy(ptr(src), ptr(dst), n, stream_of(src)), "wanmi_hbm_stream_copy")
+    return dst
+
+
+def hbm_stream_fold(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """Read ``src`` (a multiple of 32768 bytes) and write half as many bytes to ``dst`` with the
+    library's read-2-write-1 streaming kernel (``wanmi_hbm_stream_fold``: each output 16-byte word
+    is the xor of two input words), on the current stream. Measurement helper: the HBM ceiling for
+    a pass that reads two bytes per byte it writes, as the adaLN + MX pass does."""
+    lib = load()
+    if src.device.type != "cuda" or dst.device != src.device:
+        raise RuntimeError("hbm_stream_fold: src and dst must be on the same GPU; no CPU fallback")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("hbm_stream_fold: src and dst must be contiguous")
+    n = src.numel() * src.element_size()
+    if n % 32768:
+        raise ValueError("hbm_stream_fold: src must hold a multiple of 32768 bytes")
+    if dst.numel() * dst.element_size() != n // 2:
+        raise ValueError("hbm_stream_fold: dst must hold half as many bytes as src")
+    check(lib.wanmi_hbm_stream_fold(ptr(src), ptr(dst), n, stream_of(src)), "wanmi_hbm_stream_fold")
     return dst
 
 

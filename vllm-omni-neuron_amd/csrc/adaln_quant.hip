@@ -76,7 +76,7 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 // variant of the per-value math and selected among them (five v_cndmask per value).
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <int NCH, bool kLdsMod = false, int kNorm = -1>
+template <int NCH, bool kLdsMod = false, int kNorm = -1, int kQuant = -1>
 __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
   constexpr int kRows = kLdsMod ? 8 : 4;  // rows (waves) per workgroup
@@ -227,11 +227,15 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
   // for a second pass because its scale needs the whole row's max.
   const __amdgpu_buffer_rsrc_t r_m = rsrc(a.mul, 4 * (int64_t)H);
   const __amdgpu_buffer_rsrc_t r_a = rsrc(a.add, 4 * (int64_t)H);
-  const int64_t out_row_bytes = a.quant == WANMI_QUANT_NONE ? 2 * (int64_t)H
-                                : a.quant == WANMI_QUANT_MX  ? (int64_t)H
+  const int quant = kQuant >= 0 ? kQuant : a.quant;
+  const int64_t out_row_bytes = quant == WANMI_QUANT_NONE ? 2 * (int64_t)H
+                                : quant == WANMI_QUANT_MX  ? (int64_t)H
                                                              : (int64_t)H + 4;
   const __amdgpu_buffer_rsrc_t r_o =
       rsrc(reinterpret_cast<const uint8_t*>(a.out) + row * out_row_bytes, out_row_bytes);
+  // the row's e8m0 scales (MX): one byte per 32 columns; bytes past H / 32 are dropped
+  const __amdgpu_buffer_rsrc_t r_s = rsrc(quant == WANMI_QUANT_MX ? a.scales + row * (int64_t)(H / 32) : nullptr,
+                                          quant == WANMI_QUANT_MX ? H / 32 : 0);
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -273,12 +277,12 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
           y[2 * j + 1] = bf16_hi(yp[j]);
         }
       }
-      if (a.quant == WANMI_QUANT_NONE) {
+      if (quant == WANMI_QUANT_NONE) {
         u32x4 ov;
 #pragma unroll
         for (int j = 0; j < 4; ++j) ov[j] = yp[j];
         store_b128_guarded(ov, r_o, lane * 16, c * 1024);
-      } else if (a.quant == WANMI_QUANT_MX) {
+      } else if (quant == WANMI_QUANT_MX) {
         // a 32-block is 4 consecutive lanes (col / 32 == c * 16 + lane / 4)
         // the largest exponent field is that of the largest |y|: the largest (bits & 0x7fff) of
         // the packed pairs
@@ -294,7 +298,9 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
         cv[0] = cvt_e4m3x4(y[0] * f, y[1] * f, y[2] * f, y[3] * f);
         cv[1] = cvt_e4m3x4(y[4] * f, y[5] * f, y[6] * f, y[7] * f);
         __builtin_amdgcn_raw_buffer_store_b64(cv, r_o, lane * 8, c * 512, 0);
-        if (ok && (lane & 3) == 0) a.scales[row * (int64_t)(H / 32) + c * 16 + (lane >> 2)] = (uint8_t)sexp;
+        // one byte per 4 lanes; the other lanes' offsets (and those of columns past H) lie past the
+        // descriptor's extent and are dropped, so the store needs no branch
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sexp, r_s, ok && (lane & 3) == 0 ? c * 16 + (lane >> 2) : H, 0, 0);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(y[j]));
@@ -305,7 +311,7 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
   }
 
   // ---- ROW: codes = e4m3(y / dq), dq = max(amax / 448, 1e-6), fp32 dq appended ----
-  if (a.quant == WANMI_QUANT_ROW) {
+  if (quant == WANMI_QUANT_ROW) {
     amax = wave_max_f32_asc(amax);
     const float dq = fmaxf(amax / 448.0f, 1e-6f);
     // The packed row is H + 4 bytes: codes through a descriptor over H bytes, then the scale.
@@ -336,7 +342,10 @@ static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
   const int64_t blocks8 = (a.T + 7) / 8;  // the LDS instantiation: eight rows per workgroup
   if constexpr (NCH <= 10) {
     if (!a.residual && a.mul && a.add && a.H == NCH * 512) {
-      if (a.norm == WANMI_NORM_LAYER)
+      if (a.norm == WANMI_NORM_LAYER && a.quant == WANMI_QUANT_MX)
+        hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER, WANMI_QUANT_MX>), dim3((unsigned)blocks8),
+                           dim3(512), 0, stream, a);
+      else if (a.norm == WANMI_NORM_LAYER)
         hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER>), dim3((unsigned)blocks8), dim3(512), 0, stream, a);
       else if (a.norm == WANMI_NORM_RMS)
         hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_RMS>), dim3((unsigned)blocks8), dim3(512), 0, stream, a);
