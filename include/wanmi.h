@@ -292,6 +292,18 @@ int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t 
                                   int64_t o_d_stride, void* stream);
 
 /*
+ * d-major bf16 attention output -> token-major MX activation, one pass: x holds element (b, n, d, s)
+ * at x[b*b_stride + n*h_stride + d*d_stride + s] (d < 128); codes [B*S, heads*128] e4m3fn and scales
+ * [B*S, heads*4] e8m0 (one per 32 consecutive channels, the adaLN kernel's MX rule), the layout
+ * wanmi_mxfp8_gemm takes as its activation. Replaces the in-kernel quantization of the reference's
+ * ROW_MX o-projection input (row_mx_kernels.py:114-138, fed d-major by wan2_2_transformer.py:815-836).
+ * Needs S a multiple of 8, strides multiples of 8 elements with d_stride >= S, 16-byte aligned x and
+ * codes (WANMI_ERR_UNSUPPORTED otherwise).
+ */
+int wanmi_dmajor_to_mx(const void* x, int64_t B, int heads, int64_t S, int64_t b_stride, int64_t h_stride,
+                       int64_t d_stride, void* codes, uint8_t* scales, void* stream);
+
+/*
  * Streaming device-to-device copy of `bytes` (a multiple of 16; src and dst 16-byte aligned, not
  * overlapping) on `stream`: 16-byte loads, eight per thread in flight before its non-temporal
  * stores, one 32 KiB chunk per workgroup. Measurement infrastructure with no counterpart in the

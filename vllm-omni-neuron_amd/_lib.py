@@ -54,6 +54,7 @@ _SIGNATURES = {
     ],
     "wanmi_hbm_stream_copy": [_vp, _vp, _i64, _vp],
     "wanmi_hbm_stream_fold": [_vp, _vp, _i64, _vp],
+    "wanmi_dmajor_to_mx": [_vp, _i64, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "wanmi_qk_rmsnorm_rope_qrr": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp, _i64, _i32, _f32, _vp, _vp],
     "wanmi_attention_const_max_qrr": [
         _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _f32, _i32,

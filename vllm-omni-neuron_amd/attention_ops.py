@@ -434,7 +434,30 @@ def row_mx_o_proj(attention: torch.Tensor, weight: MXWeight, weight_scales: torc
     B, N, D, S = attention.shape
     if N * D != w.in_features:
         raise ValueError(f"attention has N*D = {N * D} channels, the weight contracts {w.in_features}")
-    x = attention.permute(0, 3, 1, 2).reshape(B * S, N * D).contiguous()
-    xq = adaln_quant_2d(x, None, None, eps=0.0, norm_type="none", quant="mx")
+    xq = dmajor_to_mx(attention)
     y = mxfp8_linear(xq, w)
     return y.reshape(B, S, -1)
+
+
+def dmajor_to_mx(attention: torch.Tensor) -> MXTensor:
+    """d-major bf16 ``[B, N, 128, S]`` -> the token-major MX activation ``[B*S, N*128]`` (codes + one
+    e8m0 scale per 32 channels), in one pass (``wanmi_dmajor_to_mx``) when the token axis is
+    contiguous with S and the strides multiples of 8; otherwise a transposing copy and the adaLN
+    kernel's NO_NORM / MX mode, which give the same bits."""
+    if not isinstance(attention, torch.Tensor) or attention.dim() != 4 or attention.dtype != torch.bfloat16:
+        raise ValueError("attention must be bf16 [B, N, D, S]")
+    B, N, D, S = attention.shape
+    if D != HEAD_DIM:
+        raise NotImplementedError(f"head_dim {D} (only {HEAD_DIM} is built)")
+    lib = _lib.load()
+    _lib.require_gpu(attention, what="dmajor_to_mx")
+    bs, hs, ds, ss = attention.stride()
+    if (B * S == 0 or ss != 1 or S % 8 or ds < S or bs % 8 or hs % 8 or ds % 8
+            or attention.data_ptr() % 16):
+        x = attention.permute(0, 3, 1, 2).reshape(B * S, N * D).contiguous()
+        return adaln_quant_2d(x, None, None, eps=0.0, norm_type="none", quant="mx")
+    codes = torch.empty(B * S, N * D, dtype=torch.uint8, device=attention.device)
+    scales = torch.empty(B * S, N * D // 32, dtype=torch.uint8, device=attention.device)
+    _lib.check(lib.wanmi_dmajor_to_mx(_lib.ptr(attention), B, N, S, bs, hs, ds, _lib.ptr(codes), _lib.ptr(scales),
+                                      _lib.stream_of(attention)), "wanmi_dmajor_to_mx")
+    return MXTensor(codes.view(torch.float8_e4m3fn), scales)
