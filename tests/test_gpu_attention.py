@@ -72,9 +72,24 @@ def test_transpose_heads_layout(pkg, dev):
     assert torch.equal(vt.cpu(), ref)
 
 
-def test_head_max_norm(pkg, dev):
-    k = _rand((777, 5, 128), 6, scale=2.0)
-    got = pkg.attention_ops.head_max_norm(k.to(dev)).cpu()
+@pytest.mark.parametrize("S,N,layout", [(777, 5, "token"), (1, 3, "token"), (5, 4, "token"), (4099, 40, "qkv"),
+                                         (300, 6, "head"), (32760, 40, "qkv")])
+def test_head_max_norm(pkg, dev, S, N, layout):
+    """max over tokens of each head's norm, for token-major, strided ([Q | K | V] rows) and
+    head-major K, with the largest key planted in the last token, the first, and one in between."""
+    k = _rand((S, N, 128), 6 + S, scale=2.0)
+    k[-1, 0] *= 3.0
+    k[0, N - 1] *= 3.0
+    k[S // 2, N // 2] *= 3.0
+    if layout == "token":
+        kd = k.to(dev)
+    elif layout == "qkv":
+        kd = torch.zeros(S, 3, N, 128, dtype=torch.bfloat16, device=dev)
+        kd[:, 1] = k.to(dev)
+        kd = kd[:, 1]
+    else:
+        kd = k.to(dev).permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    got = pkg.attention_ops.head_max_norm(kd).cpu()
     ref = k.float().norm(dim=-1).amax(dim=0)
     torch.testing.assert_close(got, ref, rtol=1e-5, atol=0)
 

@@ -889,31 +889,47 @@ __global__ __launch_bounds__(64) void attention_rescue_kernel(AttnArgs a) {
   }
 }
 
-// max over tokens of the per-head L2 norm of a [S, heads, 128] (strided) bf16 tensor
+// max over tokens of the per-head L2 norm of a [S, heads, 128] (strided) bf16 tensor. A token's
+// head is 16 lanes (one DPP row, 16 bytes each); a wave takes 4 consecutive tokens per step through a
+// descriptor based at its first token (the extent ends at the last valid row, so rows past S read as
+// zero and cannot raise the maximum) and issues the loads of 4 steps before reducing any (16 KiB per
+// wave in flight); the row sums use DPP moves, no LDS round trips.
 __global__ __launch_bounds__(256) void head_max_norm_kernel(const uint16_t* x, int64_t hs, int64_t ss, int64_t S,
                                                             int heads, float* out) {
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  float mx = 0.0f;
-  for (int64_t s = (int64_t)blockIdx.x * 16 + wave * 4 + (lane >> 4); s < S; s += (int64_t)gridDim.x * 16) {
-    const uint4 v = *reinterpret_cast<const uint4*>(x + h * hs + s * ss + (lane & 15) * 8);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    float n2 = 0.0f;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint16_t* xh = x + h * hs;
+  const uint32_t loff = (uint32_t)(((lane >> 4) * ss + (lane & 15) * 8) * 2);
+  float mx = 0.0f;  // max of ||x||^2 (the root taken once at the end: monotone, correctly rounded)
+  const int64_t step = (int64_t)gridDim.x * 16;
+  for (int64_t wb = (int64_t)blockIdx.x * 16 + wave * 4; wb < S; wb += 4 * step) {
+    u32x4 v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float lo = bf16_lo(w[j]), hi = bf16_hi(w[j]);
-      n2 += lo * lo + hi * hi;
+    for (int u = 0; u < 4; ++u) {
+      const int64_t b = wb + u * step;
+      const int64_t rows = S - b < 4 ? (S - b > 0 ? S - b : 0) : 4;
+      const __amdgpu_buffer_rsrc_t r = attn_rsrc(rows > 0 ? xh + b * ss : xh, rows > 0 ? ((rows - 1) * ss + 128) * 2 : 0);
+      v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, loff, 0, 0);
     }
-    n2 += __shfl_xor(n2, 1, 64);
-    n2 += __shfl_xor(n2, 2, 64);
-    n2 += __shfl_xor(n2, 4, 64);
-    n2 += __shfl_xor(n2, 8, 64);
-    mx = fmaxf(mx, sqrtf(n2));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float n2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_lo(v[u][j]), hi = bf16_hi(v[u][j]);
+        n2 += lo * lo + hi * hi;
+      }
+      n2 = n2 + dpp_f32<0xB1>(n2);   // quad_perm(1,0,3,2): xor 1
+      n2 = n2 + dpp_f32<0x4E>(n2);   // quad_perm(2,3,0,1): xor 2
+      n2 = n2 + dpp_f32<0x141>(n2);  // row_half_mirror: xor 4 on uniform quads
+      n2 = n2 + dpp_f32<0x140>(n2);  // row_mirror: xor 8 on uniform 8-lane groups
+      mx = fmaxf(mx, n2);
+    }
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(out) + h, __float_as_uint(mx));
+  if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(out) + h, __float_as_uint(sqrtf(mx)));
 }
 
 __global__ void attn_zero_kernel(float* p, int n) {
@@ -931,6 +947,11 @@ extern "C" int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t t
   WANMI_REQUIRE(out, WANMI_ERR_ARG, "wanmi_head_max_norm: out must not be null");
   WANMI_REQUIRE(head_stride % 8 == 0 && token_stride % 8 == 0, WANMI_ERR_ARG,
                 "wanmi_head_max_norm: strides must be multiples of 8 elements");
+  WANMI_REQUIRE(S <= 1 || token_stride >= 128, WANMI_ERR_ARG,
+                "wanmi_head_max_norm: token_stride=%lld must be >= 128 (tokens' head rows may not overlap)",
+                (long long)token_stride);
+  WANMI_REQUIRE((3 * token_stride + 128) * 2 < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+                "wanmi_head_max_norm: token_stride too large");
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(attn_zero_kernel, dim3((heads + 255) / 256), dim3(256), 0, s, out, heads);
   int st = check_launch("wanmi_head_max_norm(zero)");
