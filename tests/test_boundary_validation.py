@@ -257,3 +257,19 @@ def test_rope_refuses_head_dims_whose_split_disagrees(pkg, head_dim):
     with pytest.raises(NotImplementedError, match="split"):
         pkg.WanRotaryPosEmbed(head_dim, (1, 2, 2), 1024)
     pkg.WanRotaryPosEmbed(128, (1, 2, 2), 1024)  # the Wan head_dim is accepted
+
+
+def test_dmajor_to_mx_and_stream_helpers(pkg):
+    ops = pkg.attention_ops
+    with pytest.raises(ValueError, match="bf16"):
+        ops.dmajor_to_mx(torch.zeros(1, 2, 128, 8))  # fp32
+    with pytest.raises(ValueError, match="bf16"):
+        ops.dmajor_to_mx(torch.zeros(2, 128, 8, dtype=torch.bfloat16))  # rank 3
+    with pytest.raises(NotImplementedError, match="head_dim"):
+        ops.dmajor_to_mx(torch.zeros(1, 2, 64, 8, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ops.dmajor_to_mx(torch.zeros(1, 2, 128, 8, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg._lib.hbm_stream_fold(torch.zeros(16384, dtype=torch.uint8), torch.zeros(32768, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg._lib.hbm_stream_copy(torch.zeros(16, dtype=torch.uint8), torch.zeros(16, dtype=torch.uint8))
