@@ -292,6 +292,17 @@ int wanmi_attention_exact_noalloc(const void* q, int64_t q_head_stride, int64_t 
                                   int64_t o_d_stride, void* stream);
 
 /*
+ * wanmi_qk_rmsnorm_rope with the result written to `out` instead of back into x: element (token t,
+ * head h, d) at out[t*out_token_stride + h*out_head_stride + d] (strides multiples of 8 elements,
+ * out 16-byte aligned, heads <= 40). For the head-major NBSd result of the reference's projection
+ * (qkv_cte.py output_layout NBSd, row_mx_modules.py:478-507), written in the normalization pass
+ * instead of by a separate transposing copy. Bits as the in-place form.
+ */
+int wanmi_qk_rmsnorm_rope_to(const void* x, int64_t S, int64_t ld, int heads, const float* gamma, const float* cos_tab,
+                             const float* sin_tab, int rope_pairs, float eps, void* out, int64_t out_token_stride,
+                             int64_t out_head_stride, void* stream);
+
+/*
  * d-major bf16 attention output -> token-major MX activation, one pass: x holds element (b, n, d, s)
  * at x[b*b_stride + n*h_stride + d*d_stride + s] (d < 128); codes [B*S, heads*128] e4m3fn and scales
  * [B*S, heads*4] e8m0 (one per 32 consecutive channels, the adaLN kernel's MX rule), the layout

@@ -34,6 +34,7 @@ _SIGNATURES = {
     "wanmi_e4m3_encode": [_vp, _vp, _i64, _vp],
     "wanmi_mxfp8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp],
     "wanmi_qk_rmsnorm_rope": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp],
+    "wanmi_qk_rmsnorm_rope_to": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _i64, _i64, _vp],
     "wanmi_rope_tables": [_i64, _i64, _i64, _i32, _i64, ctypes.c_double, _i32, _vp, _vp, _vp],
     "wanmi_transpose_heads": [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "wanmi_head_max_norm": [_vp, _i64, _i64, _i64, _i32, _vp, _vp],

@@ -110,6 +110,38 @@ def qk_rmsnorm_rope_(x: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None
     return kmax
 
 
+def qk_rmsnorm_rope_to(x: torch.Tensor, out: torch.Tensor, gamma: torch.Tensor, *, cos=None, sin=None,
+                       eps: float = 1e-6, rope_pairs: str = "interleaved") -> torch.Tensor:
+    """:func:`qk_rmsnorm_rope_` with the result written to ``out`` instead of back into ``x``: ``out``
+    a bf16 ``[S, heads, 128]`` view with unit d stride and any token / head strides (the head-major
+    ``[heads, S, 128]`` layout as ``.permute(1, 0, 2)``, for instance), at most 40 heads. Same bits."""
+    lib = _lib.load()
+    if rope_pairs not in _ROTATE:
+        raise ValueError(f"unknown rope_pairs {rope_pairs!r}")
+    if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a bf16 [S, heads*128] view with unit column stride")
+    S, W = x.shape
+    if W % (4 * HEAD_DIM) or W > 40 * HEAD_DIM:
+        raise ValueError(f"x width {W} must be a multiple of {4 * HEAD_DIM}, at most {40 * HEAD_DIM}")
+    if x.stride(0) % 8 or x.data_ptr() % 16:
+        raise ValueError("x rows must be 16-byte aligned")
+    heads = W // HEAD_DIM
+    if not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or tuple(out.shape) != (S, heads, HEAD_DIM) \
+            or out.stride(2) != 1 or out.stride(0) % 8 or out.stride(1) % 8 or out.data_ptr() % 16:
+        raise ValueError(f"out must be a bf16 [{S}, {heads}, {HEAD_DIM}] view with unit d stride, 16-byte aligned rows")
+    if not isinstance(gamma, torch.Tensor) or gamma.numel() != W or not gamma.is_floating_point():
+        raise ValueError(f"gamma must be a floating-point tensor of {W} elements")
+    _check_rope_tables(cos, sin, S, "qk_rmsnorm_rope_to")
+    _lib.require_gpu(x, out, gamma, cos, sin, what="qk_rmsnorm_rope_to")
+    gamma = gamma.reshape(W).to(torch.float32).contiguous()
+    st = lib.wanmi_qk_rmsnorm_rope_to(
+        _lib.ptr(x), S, x.stride(0), heads, _lib.ptr(gamma), _lib.ptr(cos), _lib.ptr(sin), _ROTATE[rope_pairs],
+        float(eps), _lib.ptr(out), out.stride(0), out.stride(1), _lib.stream_of(x),
+    )
+    _lib.check(st, "wanmi_qk_rmsnorm_rope_to")
+    return out
+
+
 def transpose_heads(v: torch.Tensor):
     """bf16 ``[S, N, 128]`` (any strides with unit d stride) -> V^T ``[N, 128, S_pad]`` in the
     attention kernel's key order; returns ``(vt, S_pad)``."""
@@ -409,17 +441,35 @@ def row_mx_qkv_proj(
             raise ValueError("fused_rope needs cos_cache and sin_cache")
         cos = _base_angles(cos_cache, B, S, "cos_cache")
         sin = _base_angles(sin_cache, B, S, "sin_cache")
+    nbsd = output_layout == QKVOutputLayout.NBSd
+    # NBSd: the norm passes write their heads straight into the head-major result (up to 40 heads a
+    # pass); the other heads are copied there
+    out = torch.empty(width // head_dim, B, S, head_dim, dtype=y.dtype, device=y.device) if nbsd else None
+    direct = [False, False]
     for b in range(B):  # the caches may differ per batch element; the norm is per row
         rows = y2[b * S : (b + 1) * S]
-        if norm_q:
-            qk_rmsnorm_rope_(rows[:, : nq * head_dim], qk_norm_pre_rope_q_gamma, cos=cos[b], sin=sin[b], eps=eps,
-                             rope_pairs=w.rope_pairs)
-        if norm_k:
-            qk_rmsnorm_rope_(rows[:, nq * head_dim : (nq + nkv) * head_dim], qk_norm_pre_rope_k_gamma, cos=cos[b],
-                             sin=sin[b], eps=eps, rope_pairs=w.rope_pairs)
-    if output_layout == QKVOutputLayout.NBSd:
-        return y.reshape(*lead, width // head_dim, head_dim).movedim(-2, 0).contiguous()
-    return y
+        for i, (on, h0, nh, gam) in enumerate(((norm_q, 0, nq, qk_norm_pre_rope_q_gamma),
+                                               (norm_k, nq, nkv, qk_norm_pre_rope_k_gamma))):
+            if not on:
+                continue
+            part = rows[:, h0 * head_dim : (h0 + nh) * head_dim]
+            if nbsd and nh <= 40:
+                qk_rmsnorm_rope_to(part, out[h0 : h0 + nh, b].permute(1, 0, 2), gam, cos=cos[b], sin=sin[b], eps=eps,
+                                   rope_pairs=w.rope_pairs)
+                direct[i] = True
+            else:
+                qk_rmsnorm_rope_(part, gam, cos=cos[b], sin=sin[b], eps=eps, rope_pairs=w.rope_pairs)
+    if not nbsd:
+        return y
+    heads_all = y.reshape(B, S, width // head_dim, head_dim)
+    done = [(0, nq)] if direct[0] else []
+    done += [(nq, nq + nkv)] if direct[1] else []
+    start = 0
+    for lo, hi in done + [(width // head_dim, width // head_dim)]:
+        if lo > start:  # heads not written by a norm pass
+            out[start:lo].copy_(heads_all[:, :, start:lo].permute(2, 0, 1, 3))
+        start = hi
+    return out.reshape(width // head_dim, *lead, head_dim)
 
 
 def row_mx_o_proj(attention: torch.Tensor, weight: MXWeight, weight_scales: torch.Tensor | None = None,

@@ -44,6 +44,10 @@ struct QKNormArgs {
   int q_heads;
   float q_eps;
   float* q_rr;
+  // optional (kOut instantiation): the result goes to out instead of back into x, element
+  // (token t, head h, d) at out[t*out_ts + h*out_hs + d] (e.g. the head-major [N, S, 128] layout)
+  uint16_t* out;
+  int64_t out_ts, out_hs;
 };
 
 
@@ -56,7 +60,7 @@ struct QKNormArgs {
 // Up to 40 heads the fp32 gamma (8 bytes per column, as much as the token's own bf16 read and write)
 // is copied into LDS once per workgroup of 32 tokens instead of being read from L2 per token: per
 // chunk, every lane's first four values (16 bytes, lane-major), then the second four.
-template <int NCH, bool kHalves>
+template <int NCH, bool kHalves, bool kOut = false>
 __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kernel(QKNormArgs a) {
 #pragma clang fp contract(off)
   constexpr bool kLdsGamma = NCH <= 10;
@@ -201,7 +205,14 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
             n2 = n2 + fb * fb;
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
+        if constexpr (kOut) {
+          // head c * 4 + (lane >> 4) of the chunk: 16 lanes write its 256 bytes, through a descriptor
+          // based at the token (the host keeps every offset below 2^31)
+          const __amdgpu_buffer_rsrc_t r_o = make_rsrc(a.out + t * a.out_ts, ((a.heads - 1) * a.out_hs + 128) * 2);
+          store_b128_guarded(ov, r_o, (int)(((lane >> 4) * a.out_hs + (lane & 15) * 8) * 2), (int)(c * 8 * a.out_hs));
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
+        }
         if (a.maxnorm) {
           // one head = 16 consecutive lanes of a chunk (one DPP row): sum over the row with DPP
           // moves (quad xor 1, quad xor 2, half-row mirror, row mirror -- the pairs of an xor 1, 2,
@@ -292,7 +303,8 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(TransposeArgs a) {
 namespace wanmi {
 static int qk_rmsnorm_rope_impl(void* x, int64_t S, int64_t ld, int heads, const float* gamma, const float* cos_tab,
                                 const float* sin_tab, int rope_pairs, float eps, float* maxnorm, const float* q_sumsq,
-                                int64_t q_sumsq_ld, int q_heads, float q_eps, float* q_rr, void* stream) {
+                                int64_t q_sumsq_ld, int q_heads, float q_eps, float* q_rr, void* stream,
+                                void* out = nullptr, int64_t out_ts = 0, int64_t out_hs = 0) {
   WANMI_REQUIRE(S >= 0 && heads > 0 && heads % 4 == 0 && heads <= 128, WANMI_ERR_ARG,
                 "wanmi_qk_rmsnorm_rope: need S >= 0 and heads a positive multiple of 4 (<= 128), got S=%lld heads=%d",
                 (long long)S, heads);
@@ -330,8 +342,22 @@ static int qk_rmsnorm_rope_impl(void* x, int64_t S, int64_t ld, int heads, const
   a.q_heads = q_heads;
   a.q_eps = q_eps;
   a.q_rr = q_rr;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_ts = out_ts;
+  a.out_hs = out_hs;
   const int64_t waves = (S + a.tokens_per_wave - 1) / a.tokens_per_wave;
   const dim3 grid((unsigned)((waves + 3) / 4));
+  if (out) {
+    WANMI_REQUIRE(a.nch <= 10, WANMI_ERR_UNSUPPORTED, "wanmi_qk_rmsnorm_rope_to: at most 40 heads");
+    if (rope_pairs == WANMI_ROTATE_HALVES) {
+      if (a.nch <= 4) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<4, true, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<10, true, true>), grid, dim3(256), 0, s, a);
+    } else {
+      if (a.nch <= 4) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<4, false, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<10, false, true>), grid, dim3(256), 0, s, a);
+    }
+    return check_launch("wanmi_qk_rmsnorm_rope_to");
+  }
   if (rope_pairs == WANMI_ROTATE_HALVES) {
     if (a.nch <= 4) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<4, true>), grid, dim3(256), 0, s, a);
     else if (a.nch <= 10) hipLaunchKernelGGL(HIP_KERNEL_NAME(qk_rmsnorm_rope_kernel<10, true>), grid, dim3(256), 0, s, a);
@@ -353,6 +379,21 @@ extern "C" int wanmi_qk_rmsnorm_rope(void* x, int64_t S, int64_t ld, int heads, 
   wanmi::clear_error();
   return wanmi::qk_rmsnorm_rope_impl(x, S, ld, heads, gamma, cos_tab, sin_tab, rope_pairs, eps, maxnorm, nullptr, 0, 0,
                                      0.0f, nullptr, stream);
+}
+
+extern "C" int wanmi_qk_rmsnorm_rope_to(const void* x, int64_t S, int64_t ld, int heads, const float* gamma,
+                                        const float* cos_tab, const float* sin_tab, int rope_pairs, float eps,
+                                        void* out, int64_t out_token_stride, int64_t out_head_stride, void* stream) {
+  using namespace wanmi;
+  clear_error();
+  WANMI_REQUIRE(out && ((uintptr_t)out % 16) == 0 && out_token_stride % 8 == 0 && out_head_stride % 8 == 0 &&
+                    out_token_stride >= 0 && out_head_stride >= 0,
+                WANMI_ERR_ARG,
+                "wanmi_qk_rmsnorm_rope_to: out must be 16-byte aligned with strides that are multiples of 8 elements");
+  WANMI_REQUIRE(heads > 0 && ((int64_t)(heads - 1) * out_head_stride + 128) * 2 < (1LL << 31), WANMI_ERR_UNSUPPORTED,
+                "wanmi_qk_rmsnorm_rope_to: one token's heads span more than 2 GiB of out");
+  return qk_rmsnorm_rope_impl(const_cast<void*>(x), S, ld, heads, gamma, cos_tab, sin_tab, rope_pairs, eps, nullptr,
+                              nullptr, 0, 0, 0.0f, nullptr, stream, out, out_token_stride, out_head_stride);
 }
 
 extern "C" int wanmi_qk_rmsnorm_rope_qrr(void* x, int64_t S, int64_t ld, int heads, const float* gamma,
