@@ -57,22 +57,31 @@ def test_adaln_modes_bit_exact(pkg, dev, norm_type, quant):
         np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), ref["packed"])
 
 
+@pytest.mark.parametrize("quant,norm", [("mx", "layer_norm"), ("row", "layer_norm"), ("none", "rms_norm"),
+                                        ("row", "none")])
 @pytest.mark.parametrize("with_gate", [True, False])
-def test_adaln_fused_residual_bit_exact(pkg, dev, with_gate):
+def test_adaln_fused_residual_bit_exact(pkg, dev, with_gate, quant, norm):
+    """The reference's residual sites: x = bf16(h * gate + res) (gate optional), written out, then
+    normalized, modulated and quantized; 300 rows (a partial workgroup of eight at the end)."""
     T, H = 300, 5120
     x, mul, add, res, gate = _inputs(T, H, seed=5, residual=True)
     gate = gate if with_gate else None
     res_out, out = pkg.adaln_modulate(
-        x.to(dev), mul.to(dev), add.to(dev), eps=1e-6, quant="mx", residual=res.to(dev),
+        x.to(dev), mul.to(dev), add.to(dev), eps=1e-6, norm_type=norm, quant=quant, residual=res.to(dev),
         gate=None if gate is None else gate.to(dev),
     )
     ref = oracle_adaln.adaln_quant(
-        _np(x), mul.numpy(), add.numpy(), eps=1e-6, quant="mx", residual=_np(res),
+        _np(x), mul.numpy(), add.numpy(), eps=1e-6, norm_type=norm, quant=quant, residual=_np(res),
         gate=None if gate is None else gate.numpy(),
     )
     np.testing.assert_array_equal(res_out.float().cpu().numpy(), ref["residual_out"])
-    np.testing.assert_array_equal(out.scales.cpu().numpy(), ref["scales"])
-    np.testing.assert_array_equal(out.codes.view(torch.uint8).cpu().numpy(), ref["codes"])
+    if quant == "mx":
+        np.testing.assert_array_equal(out.scales.cpu().numpy(), ref["scales"])
+        np.testing.assert_array_equal(out.codes.view(torch.uint8).cpu().numpy(), ref["codes"])
+    elif quant == "row":
+        np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), ref["packed"])
+    else:
+        np.testing.assert_array_equal(out.float().cpu().numpy(), ref["y"])
 
 
 def test_adaln_batched_modulation(pkg, dev):

@@ -76,11 +76,12 @@ __device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int lane, int c
 // variant of the per-value math and selected among them (five v_cndmask per value).
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <int NCH, bool kLdsMod = false, int kNorm = -1, int kQuant = -1>
+template <int NCH, bool kLdsMod = false, int kNorm = -1, int kQuant = -1, bool kRes = false>
 __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 : 2)) void adaln_quant_kernel(AdalnArgs a) {
 #pragma clang fp contract(off)
   constexpr int kRows = kLdsMod ? 8 : 4;  // rows (waves) per workgroup
-  __shared__ __attribute__((aligned(16))) float smod[kLdsMod ? 2 * 2 * NCH * 64 * 4 : 4];
+  constexpr int kVecs = kRes ? 3 : 2;     // vectors in LDS: mul, add (and the residual gate)
+  __shared__ __attribute__((aligned(16))) float smod[kLdsMod ? kVecs * 2 * NCH * 64 * 4 : 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.H;
@@ -94,6 +95,7 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
 
   const __amdgpu_buffer_rsrc_t r_x = rsrc(a.hidden + rbase, live ? 2 * (int64_t)H : 0);
   uint32_t xp[NCH][4];  // the row's x as packed bf16 pairs (exact; also the residual sum)
+  [[maybe_unused]] uint32_t rp[kRes ? NCH : 1][4];  // kRes: the residual row, combined after the barrier
 
   // ---- load (and optional gated residual add, x = bf16(h * gate + res)) ----
   if (!kLdsMod && a.residual) {
@@ -125,10 +127,17 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
       }
     }
   } else {
+    [[maybe_unused]] const __amdgpu_buffer_rsrc_t r_r = rsrc(kRes && live ? a.residual + rbase : nullptr,
+                                                            kRes && live ? 2 * (int64_t)H : 0);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (c < nch) {
         const u32x4 hv = __builtin_amdgcn_raw_buffer_load_b128(r_x, lane * 16, c * 1024, 0);
+        if constexpr (kRes) {
+          const u32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(r_r, lane * 16, c * 1024, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rp[c][j] = rv[j];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) xp[c][j] = hv[j];
       } else {
@@ -142,13 +151,43 @@ __global__ __launch_bounds__(kLdsMod ? 512 : 256, kLdsMod ? 1 : (NCH <= 10 ? 4 :
     constexpr int kPerVec = 2 * NCH;  // 1 KiB loads per vector: halves x chunks
     const uint32_t base = lds_addr(smod);
     const u32x4 rm = buffer_rsrc(a.mul, 4u * (uint32_t)H), ra = buffer_rsrc(a.add, 4u * (uint32_t)H);
-    for (int k = wave; k < 2 * kPerVec; k += kRows) {
+    // kRes: the gate is the third vector (all ones when absent: its loads read past an empty extent
+    // as zero, so it is not used then)
+    [[maybe_unused]] const u32x4 rgt = buffer_rsrc(a.gate, a.gate ? 4u * (uint32_t)H : 0u);
+    for (int k = wave; k < kVecs * kPerVec; k += kRows) {
       const int kk = k % kPerVec, hh = kk / NCH, c = kk % NCH;
-      lds_dma_b128(k < kPerVec ? rm : ra, (uint32_t)(c * 512 + 8 * lane + 4 * hh) * 4, base + (uint32_t)k * 1024);
+      const u32x4 rv = k < kPerVec ? rm : (k < 2 * kPerVec ? ra : rgt);
+      lds_dma_b128(rv, (uint32_t)(c * 512 + 8 * lane + 4 * hh) * 4, base + (uint32_t)k * 1024);
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
     if (!live) return;
+    if constexpr (kRes) {
+      // x = bf16(h * gate + res) (the residual branch above, with the gate from LDS), written to
+      // residual_out and normalized below
+      const __amdgpu_buffer_rsrc_t r_ro = rsrc(a.residual_out + rbase, 2 * (int64_t)H);
+      const float4* sm = reinterpret_cast<const float4*>(smod);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float gv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        if (a.gate) {
+          const float4 g0 = sm[(4 * NCH + c) * 64 + lane], g1 = sm[(5 * NCH + c) * 64 + lane];
+          gv[0] = g0.x, gv[1] = g0.y, gv[2] = g0.z, gv[3] = g0.w, gv[4] = g1.x, gv[5] = g1.y, gv[6] = g1.z, gv[7] = g1.w;
+        }
+        u32x4 ov;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float h0 = bf16_lo(xp[c][j]), h1 = bf16_hi(xp[c][j]);
+          if (a.gate) {
+            h0 = h0 * gv[2 * j];
+            h1 = h1 * gv[2 * j + 1];
+          }
+          ov[j] = pack_bf16x2(h0 + bf16_lo(rp[c][j]), h1 + bf16_hi(rp[c][j]));
+          xp[c][j] = ov[j];
+        }
+        store_b128_guarded(ov, r_ro, lane * 16, c * 1024);
+      }
+    }
   }
 
   const int norm = kNorm >= 0 ? kNorm : a.norm;
@@ -341,6 +380,22 @@ static void launch_adaln(const AdalnArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.T + 3) / 4;
   const int64_t blocks8 = (a.T + 7) / 8;  // the LDS instantiation: eight rows per workgroup
   if constexpr (NCH <= 10) {
+    if constexpr (NCH == 10) {
+      // the reference's residual sites (gated or not) with both modulation vectors, all three
+      // vectors in LDS
+      if (a.residual && a.mul && a.add && a.H == NCH * 512) {
+        if (a.norm == WANMI_NORM_LAYER)
+          hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER, -1, true>), dim3((unsigned)blocks8),
+                             dim3(512), 0, stream, a);
+        else if (a.norm == WANMI_NORM_RMS)
+          hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_RMS, -1, true>), dim3((unsigned)blocks8),
+                             dim3(512), 0, stream, a);
+        else
+          hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_NONE, -1, true>), dim3((unsigned)blocks8),
+                             dim3(512), 0, stream, a);
+        return;
+      }
+    }
     if (!a.residual && a.mul && a.add && a.H == NCH * 512) {
       if (a.norm == WANMI_NORM_LAYER && a.quant == WANMI_QUANT_MX)
         hipLaunchKernelGGL((adaln_quant_kernel<NCH, true, WANMI_NORM_LAYER, WANMI_QUANT_MX>), dim3((unsigned)blocks8),
