@@ -611,7 +611,7 @@ __device__ __forceinline__ void epilogue_vt(const GemmArgs& g, const f32x16 (&ac
       for (int it = 0; it < 8; ++it) {
         const uint32_t d = (uint32_t)((b * 8 + it) * 8 + (lane >> 3));
         // an offset past the resource's extent drops the store (segments at or past vt_ld);
-        // non-temporal, as the other epilogues' outputs (through L2: 4% slower QKV pair)
+        // non-temporal, as the other epilogues' outputs (through L2 the QKV pair ran 0.5% slower)
         const uint32_t off = in_row ? d * (uint32_t)g.vt_ld * 2 + col_bytes : 0xFFFFFFF0u;
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{dv[it].x, dv[it].y, dv[it].z, dv[it].w}, vrsrc, (int)off, 0, 2);
       }

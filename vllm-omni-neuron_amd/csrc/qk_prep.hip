@@ -211,8 +211,7 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
           const __amdgpu_buffer_rsrc_t r_o = make_rsrc(a.out + t * a.out_ts, ((a.heads - 1) * a.out_hs + 128) * 2);
           store_b128_guarded(ov, r_o, (int)(((lane >> 4) * a.out_hs + (lane & 15) * 8) * 2), (int)(c * 8 * a.out_hs));
         } else {
-          // non-temporal (streamed past L2; 144.8 -> 136.5 us at S = 32760, same bits)
-          __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 2);
+          __builtin_amdgcn_raw_buffer_store_b128(ov, r_x, lane * 16, c * 1024, 0);
         }
         if (a.maxnorm) {
           // one head = 16 consecutive lanes of a chunk (one DPP row): sum over the row with DPP
