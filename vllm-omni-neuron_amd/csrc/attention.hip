@@ -934,6 +934,65 @@ __global__ __launch_bounds__(256) void head_max_norm_kernel(const uint16_t* x, i
   if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(out) + h, __float_as_uint(sqrtf(mx)));
 }
 
+// The same maximum when a token's heads are contiguous (head stride 128, heads a multiple of 4, at
+// most 40): a wave reads whole token rows (heads x 256 bytes, 1 KiB = 4 heads per instruction, all
+// loads of two tokens in flight) instead of one head's 256 bytes per token row, so the reads are
+// sequential; lane group l >> 4 of chunk c holds head 4 c + (l >> 4). Each wave keeps per-head maxima
+// of ||x||^2 in registers; the workgroup reduces them through LDS and issues one atomic per head.
+constexpr int kHmnRowWaves = 4;
+__global__ __launch_bounds__(256) void head_max_norm_rows_kernel(const uint16_t* x, int64_t ss, int64_t S, int heads,
+                                                                 float* out) {
+  __shared__ float smax[kHmnRowWaves][40];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nch = heads / 4;
+  float kmx[10];
+#pragma unroll
+  for (int c = 0; c < 10; ++c) kmx[c] = 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * kHmnRowWaves;
+  for (int64_t t = (int64_t)blockIdx.x * kHmnRowWaves + wave; t < S; t += 2 * stride) {
+    u32x4 v[2][10];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t tt = t + u * stride;
+      // a second token past S: an empty extent, its loads read zero
+      const __amdgpu_buffer_rsrc_t r = attn_rsrc(tt < S ? x + tt * ss : x, tt < S ? heads * 256 : 0);
+#pragma unroll
+      for (int c = 0; c < 10; ++c)
+        v[u][c] = c < nch ? __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, c * 1024, 0) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < 10; ++c) {
+        float n2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = bf16_lo(v[u][c][j]), hi = bf16_hi(v[u][c][j]);
+          n2 += lo * lo + hi * hi;
+        }
+        n2 = n2 + dpp_f32<0xB1>(n2);   // xor 1
+        n2 = n2 + dpp_f32<0x4E>(n2);   // xor 2
+        n2 = n2 + dpp_f32<0x141>(n2);  // xor 4 on uniform quads
+        n2 = n2 + dpp_f32<0x140>(n2);  // xor 8 on uniform 8-lane groups
+        kmx[c] = fmaxf(kmx[c], n2);
+      }
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int c = 0; c < 10; ++c)
+      if (c < nch) smax[wave][4 * c + (lane >> 4)] = kmx[c];
+  }
+  __syncthreads();
+  const int hd = threadIdx.x;
+  if (hd < heads) {
+    float m = smax[0][hd];
+#pragma unroll
+    for (int w = 1; w < kHmnRowWaves; ++w) m = fmaxf(m, smax[w][hd]);
+    atomicMax(reinterpret_cast<unsigned int*>(out) + hd, __float_as_uint(sqrtf(m)));
+  }
+}
+
 __global__ void attn_zero_kernel(float* p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.0f;
@@ -959,6 +1018,13 @@ extern "C" int wanmi_head_max_norm(const void* x, int64_t head_stride, int64_t t
   int st = check_launch("wanmi_head_max_norm(zero)");
   if (st || S == 0) return st;
   WANMI_REQUIRE(x && ((uintptr_t)x % 16) == 0, WANMI_ERR_ARG, "wanmi_head_max_norm: x must be 16-byte aligned");
+  if (head_stride == 128 && heads % 4 == 0 && heads <= 40 && token_stride >= heads * 128) {
+    // heads contiguous within a token: whole rows per wave (two tokens per step, so 8 per workgroup)
+    const int64_t blocks = min((S + 2 * kHmnRowWaves - 1) / (2 * kHmnRowWaves), (int64_t)1024);
+    hipLaunchKernelGGL(head_max_norm_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), token_stride, S, heads, out);
+    return check_launch("wanmi_head_max_norm");
+  }
   const int64_t blocks = min((S + 15) / 16, (int64_t)256);
   hipLaunchKernelGGL(head_max_norm_kernel, dim3((unsigned)blocks, (unsigned)heads), dim3(256), 0, s,
                      static_cast<const uint16_t*>(x), head_stride, token_stride, S, heads, out);
