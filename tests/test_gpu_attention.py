@@ -59,11 +59,23 @@ def test_attention_core_small(pkg, dev, Sq, Sk, N):
     np.testing.assert_array_equal(mx.scales.cpu().numpy(), scales)
 
 
-def test_transpose_heads_layout(pkg, dev):
-    S, N = 100, 3
-    v = _rand((S, N, 128), 5)
-    vt, S_pad = pkg.attention_ops.transpose_heads(v.to(dev))
-    assert S_pad == 128
+@pytest.mark.parametrize("S,N,layout", [(100, 3, "token"), (100, 8, "token"), (1560, 40, "qkv"), (77, 4, "head"),
+                                         (64, 4, "token")])
+def test_transpose_heads_layout(pkg, dev, S, N, layout):
+    """V^T in the attention's key order, for per-head rows (3 heads, head-major) and the four-head
+    form (heads contiguous in a token: token-major and the [Q | K | V] rows), with a partial last
+    64-key tile."""
+    v = _rand((S, N, 128), 5 + S + N)
+    if layout == "token":
+        vd = v.to(dev)
+    elif layout == "qkv":
+        vd = torch.zeros(S, 3, N, 128, dtype=torch.bfloat16, device=dev)
+        vd[:, 2] = v.to(dev)
+        vd = vd[:, 2]
+    else:
+        vd = v.to(dev).permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    vt, S_pad = pkg.attention_ops.transpose_heads(vd)
+    assert S_pad == (S + 63) // 64 * 64
     order = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
     slot_key = torch.tensor([16 * (s // 16) + order[s % 16] for s in range(S_pad)])
     ref = torch.zeros(N, 128, S_pad, dtype=torch.bfloat16)
