@@ -9,9 +9,11 @@ FP8 recipe (ROW activations, drop-ins composed as its modules call them; ``row_r
 40-block forward is measured at 720p (21x45x80 = 75600 tokens; ``p720``). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
 seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic data.
 
-Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). Per-kernel times
-come from HIP events recorded around every launch inside the timed steps; the roofline entry is the
-dominant kernel (self-attention). The CPU baseline is the reference's BF16 eager block (restated
+Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). The roofline entry
+is the dominant kernel (self-attention), timed by HIP events around each of its launches inside the
+timed steps; the other kernels' times come from events around every launch of one more forward
+after the timed steps (an event pair between two kernels idles the GPU for about 10 us, so the
+timed steps carry no others). The CPU baseline is the reference's BF16 eager block (restated
 in the oracle) timed on this host's cores at the 1560-token block shape, extrapolated to the step.
 """
 
@@ -71,14 +73,21 @@ def load_traffic(seq_len):
 
 
 class KernelTimer:
-    """Records HIP events (on the launching stream) around each kernel call of the timed steps."""
+    """Records HIP events (on the launching stream) around the kernel calls named in `only` (every
+    call when None) while active.
 
-    def __init__(self):
+    An event pair between two kernels leaves the GPU idle for about 10.6 us (kernel trace of a
+    block: back-to-back launches start 0 us apart, launches separated by an end and a start event
+    10-11 us apart), so the timed steps record only the self-attention (the roofline kernel) and
+    the other kernels are timed in one instrumented forward after them (`instrumented`)."""
+
+    def __init__(self, only=None):
         self.active = False
+        self.only = only
         self.events = {}
 
     def __call__(self, name, fn):
-        if not self.active:
+        if not self.active or (self.only is not None and name not in self.only):
             return fn()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
@@ -89,6 +98,16 @@ class KernelTimer:
 
     def summary(self):
         return {k: [s.elapsed_time(e) for s, e in v] for k, v in self.events.items()}
+
+
+def instrumented(forward):
+    """One more forward after the timed steps with events around every kernel call: the components'
+    per-launch times (each list holds one entry per launch of that forward)."""
+    timer = KernelTimer()
+    timer.active = True
+    forward(timer)
+    torch.cuda.synchronize()
+    return timer.summary()
 
 
 def gemm_flops(S):
@@ -162,7 +181,8 @@ def cpu_baseline(S_full, blocks):
 def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
     """The 40-block forward at the 720p step's length (21x45x80 = 75600 tokens, 512 text tokens, the
     same weights and cached text K/V), measured after the main metric: `warmup` untimed forwards,
-    then `steps` timed ones bracketed by device synchronizations, with per-kernel HIP events."""
+    then `steps` timed ones bracketed by device synchronizations (HIP events around the
+    self-attention only), then one instrumented forward for the other kernels' times."""
     blk = pkg.block
     grid = (21, 45, 80)
     S7 = grid[0] * grid[1] * grid[2]
@@ -170,7 +190,7 @@ def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
     h = torch.randn(S7, DIM, device=dev, generator=gen).to(torch.bfloat16)
     for _ in range(warmup):
         blk.dit_forward(blocks, h, temb, grid, crosses, tables=tables)
-    timer = KernelTimer()
+    timer = KernelTimer(only={"self_attention"})
     timer.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -180,12 +200,11 @@ def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
     ms = (time.perf_counter() - t0) * 1000.0 / steps
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite 720p DiT output")
-    times = timer.summary()
-    comp = {k: round(sum(v) / steps, 2) for k, v in sorted(times.items())}
-    attn = times["self_attention"]
+    attn = timer.summary()["self_attention"]
     attn_ms = sum(attn) / len(attn)
-    n_blk = steps * len(blocks)
-    gemm_ms = sum(sum(v) for k, v in times.items() if k.startswith("gemm_")) / n_blk
+    times = instrumented(lambda t: blk.dit_forward(blocks, h, temb, grid, crosses, timer=t, tables=tables))
+    comp = {k: round(sum(v), 2) for k, v in sorted(times.items())}
+    gemm_ms = sum(sum(v) for k, v in times.items() if k.startswith("gemm_")) / len(blocks)
     return {
         "workload": f"Wan2.2-A14B DiT forward at 720p: {len(blocks)} blocks, 21x45x80 = 75600 tokens, 512 text tokens",
         "seq_len": S7, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 1),
@@ -198,22 +217,21 @@ def step_720p(pkg, blocks, crosses, tables, temb, dev, steps=2, warmup=1):
 def row_recipe_step(pkg, row_blocks, row_crosses, tables, temb, h0, grid, steps=2, warmup=1):
     """The reference's own FP8 recipe (ROW activations at every adaLN site, per-tensor FP8 weights
     with per-channel scales, the drop-ins composed as its FP8 modules call them) over the same 40
-    blocks at the metric's length: `warmup` untimed forwards, then `steps` timed ones, with
-    per-step HIP events."""
+    blocks at the metric's length: `warmup` untimed forwards, then `steps` timed ones bracketed by
+    device synchronizations, then one instrumented forward for the per-drop-in times."""
     rb = pkg.row_block
     for _ in range(warmup):
         rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, tables=tables)
-    timer = KernelTimer()
-    timer.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        out = rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, timer=timer, tables=tables)
+        out = rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, tables=tables)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / steps
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite ROW-recipe DiT output")
-    comp = {k: round(sum(v) / steps, 2) for k, v in sorted(timer.summary().items())}
+    times = instrumented(lambda t: rb.row_dit_forward(row_blocks, h0, temb, grid, row_crosses, timer=t, tables=tables))
+    comp = {k: round(sum(v), 2) for k, v in sorted(times.items())}
     return {
         "workload": (f"the reference's FP8 block recipe (ROW activations, per-tensor FP8 weights with per-channel "
                      f"scales, drop-ins composed as row_mx_modules.py calls them), {len(row_blocks)} blocks at "
@@ -297,7 +315,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    timer = KernelTimer()
+    timer = KernelTimer(only={"self_attention"})  # the roofline kernel, timed live in the timed steps
     for _ in range(args.warmup):
         blk.dit_forward(blocks, h0, temb, grid, crosses, tables=tables)
     torch.cuda.synchronize()
@@ -314,17 +332,14 @@ def main():
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite DiT output")
 
-    times = timer.summary()
-    n_blk = args.steps * args.blocks
-
-    def avg(name):
-        return sum(times[name]) / len(times[name])
-
+    attn = timer.summary()["self_attention"]
     attn_flops = 4.0 * S * S * HEAD_DIM * HEADS
-    attn_ms = avg("self_attention")
+    attn_ms = sum(attn) / len(attn)
     attn_tflops = attn_flops / attn_ms / 1e9
+    # every other kernel: one instrumented forward after the timed steps
+    times = instrumented(lambda t: blk.dit_forward(blocks, h0, temb, grid, crosses, timer=t, tables=tables))
     gemm_names = [k for k in times if k.startswith("gemm_")]
-    gemm_ms = sum(sum(times[k]) for k in gemm_names) / n_blk
+    gemm_ms = sum(sum(times[k]) for k in gemm_names) / args.blocks
     gemm_tflops = gemm_flops(S) / gemm_ms / 1e9
     # adaLN: every launch reads x (bf16) and the two modulation / affine vectors and writes MX codes
     # and scales (the residual adds run in the GEMM epilogues)
@@ -332,8 +347,10 @@ def main():
     ad = times["adaln"]
     adaln_gbs = plain * len(ad) / sum(ad) / 1e6
     first_adaln_us = sum(ad[0::3]) / len(ad[0::3]) * 1000.0
-    comp = {k: {"ms_per_launch": round(sum(v) / len(v), 4), "ms_per_step": round(sum(v) / args.steps, 2)}
+    comp = {k: {"ms_per_launch": round(sum(v) / len(v), 4), "ms_per_step": round(sum(v), 2)}
             for k, v in sorted(times.items())}
+    # the self-attention entry from the timed steps' own events
+    comp["self_attention"] = {"ms_per_launch": round(attn_ms, 4), "ms_per_step": round(sum(attn) / args.steps, 2)}
 
     result = {
         "metric": "DiT step ms @32760 tok (A14B); attn+GEMM TFLOP/s; adaLN-quant GB/s",
