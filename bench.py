@@ -12,8 +12,7 @@ seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic 
 Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). The roofline entry
 is the dominant kernel (self-attention), timed by HIP events around each of its launches inside the
 timed steps; the other kernels' times come from events around every launch of one more forward
-after the timed steps (an event pair between two kernels idles the GPU for about 10 us, so the
-timed steps carry no others). The CPU baseline is the reference's BF16 eager block (restated
+after the timed steps (events around every launch would add about 2.5 ms to the step). The CPU baseline is the reference's BF16 eager block (restated
 in the oracle) timed on this host's cores at the 1560-token block shape, extrapolated to the step.
 """
 
@@ -76,10 +75,11 @@ class KernelTimer:
     """Records HIP events (on the launching stream) around the kernel calls named in `only` (every
     call when None) while active.
 
-    An event pair between two kernels leaves the GPU idle for about 10.6 us (kernel trace of a
-    block: back-to-back launches start 0 us apart, launches separated by an end and a start event
-    10-11 us apart), so the timed steps record only the self-attention (the roofline kernel) and
-    the other kernels are timed in one instrumented forward after them (`instrumented`)."""
+    Events around every launch of the 40-block forward cost about 2.5 ms per step (one process,
+    four interleaved two-step runs each: 988.7 ms with events around every launch, 987.0 around the
+    self-attention only, 986.1 with none), so the timed steps record only the self-attention (the
+    roofline kernel) and the other kernels are timed in one instrumented forward after them
+    (`instrumented`)."""
 
     def __init__(self, only=None):
         self.active = False
