@@ -338,9 +338,10 @@ __global__ __launch_bounds__(kThreads) void attention_const_max_kernel(AttnArgs 
       const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float a0 = round_bf16((bf16_lo(qv[t][j]) * rr) * gv[2 * j]);
-        float b0 = round_bf16((bf16_hi(qv[t][j]) * rr) * gv[2 * j + 1]);
+        float a0 = (bf16_lo(qv[t][j]) * rr) * gv[2 * j];
+        float b0 = (bf16_hi(qv[t][j]) * rr) * gv[2 * j + 1];
         if (qrope) {
+          round_bf16_pair(a0, b0);
           const float c = __uint_as_float(cv[t][j]), sn = __uint_as_float(sv[t][j]);
           const float ac = a0 * c, bs = b0 * sn, as = a0 * sn, bc = b0 * c;
           a0 = ac - bs;
@@ -642,9 +643,8 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
         const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float a0 = round_bf16((bf16_lo(qv[t][j]) * rr) * gv[2 * j]);
-          const float b0 = round_bf16((bf16_hi(qv[t][j]) * rr) * gv[2 * j + 1]);
-          qv[t][j] = pack_bf16x2(a0, b0);
+          // one rounding to bf16: the pack is the reference's rounding after the norm
+          qv[t][j] = pack_bf16x2((bf16_lo(qv[t][j]) * rr) * gv[2 * j], (bf16_hi(qv[t][j]) * rr) * gv[2 * j + 1]);
         }
       }
     }

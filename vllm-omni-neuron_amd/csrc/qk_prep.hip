@@ -89,12 +89,32 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
     // and the root taken in fp64 -- the operations, in the order, the attention's Q load performs on
     // the same partials (so the attention may read this instead, bit for bit)
     const int64_t tq = t0 + lane;
-    if (lane < a.tokens_per_wave && tq < a.S) {
+    const bool ok = lane < a.tokens_per_wave && tq < a.S;
+    float qs = 0.0f;
+    if (a.q_heads <= 40 && (a.qss_ld & 3) == 0) {
+      // all ten 16-byte loads of the row in flight at once (a loop of dependent loads would wait a
+      // memory round trip per partial before the wave's first token), through a descriptor over
+      // the wave's rows whose last row ends at q_heads rounded up to 4 (within the row, as qss_ld
+      // is a multiple of 4): lanes past the last token read zeros, and only the first q_heads
+      // values are added
+      const int64_t rows = min((int64_t)a.tokens_per_wave, a.S - t0);
+      const int64_t qh4 = (a.q_heads + 3) & ~3;
+      const __amdgpu_buffer_rsrc_t r_q =
+          make_rsrc(a.q_sumsq + (rows > 0 ? t0 * a.qss_ld : 0), rows > 0 ? ((rows - 1) * a.qss_ld + qh4) * 4 : 0);
+      u32x4 pv[10];
+#pragma unroll
+      for (int i = 0; i < 10; ++i)
+        pv[i] = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((lane * a.qss_ld + 4 * i) * 4), 0, 0);
+#pragma unroll
+      for (int i = 0; i < 10; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (4 * i + j < a.q_heads) qs = qs + __uint_as_float(pv[i][j]);
+    } else if (ok) {
       const float* pq = a.q_sumsq + tq * a.qss_ld;
-      float qs = 0.0f;
       for (int b = 0; b < a.q_heads; ++b) qs = qs + pq[b];
-      a.q_rr[tq] = (float)(1.0 / sqrt((double)(qs / (float)(a.q_heads * 128)) + (double)a.q_eps));
     }
+    if (ok) a.q_rr[tq] = (float)(1.0 / sqrt((double)(qs / (float)(a.q_heads * 128)) + (double)a.q_eps));
   }
 
   for (int it = 0; it < a.tokens_per_wave; ++it) {
@@ -167,8 +187,9 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
         if constexpr (!kHalves) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            float a0 = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
-            float b0 = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
+            float a0 = (bf16_lo(xp[c][j]) * rs) * gv[2 * j];
+            float b0 = (bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1];
+            round_bf16_pair(a0, b0);
             if (a.cos) {
               const float ac = a0 * cs[j], bs = b0 * sn[j], as = a0 * sn[j], bc = b0 * cs[j];
               const float r0 = ac - bs, r1 = as + bc;
@@ -184,8 +205,9 @@ __global__ __launch_bounds__(256, (NCH <= 10 ? 4 : 2)) void qk_rmsnorm_rope_kern
           float y[8];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            y[2 * j] = round_bf16((bf16_lo(xp[c][j]) * rs) * gv[2 * j]);
-            y[2 * j + 1] = round_bf16((bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1]);
+            y[2 * j] = (bf16_lo(xp[c][j]) * rs) * gv[2 * j];
+            y[2 * j + 1] = (bf16_hi(xp[c][j]) * rs) * gv[2 * j + 1];
+            round_bf16_pair(y[2 * j], y[2 * j + 1]);
           }
           if (a.cos) {
             // pairs (i, i+64): first half x cos - x' sin, second half x cos + x' sin (x' = the

@@ -54,7 +54,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
-__device__ __forceinline__ float round_bf16(float f) { return bf16_lo(pack_bf16x2(f, 0.0f)); }
+// Two values rounded to bf16 (round to nearest even, each on its own) by one packed conversion.
+__device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
+  const uint32_t p = pack_bf16x2(a, b);
+  a = bf16_lo(p);
+  b = bf16_hi(p);
+}
 
 // Biased fp32 exponent field of |f| (0 for zeros and subnormals), the MX block-max input.
 __device__ __forceinline__ int exp_field(float f) { return (int)((__float_as_uint(f) >> 23) & 0xFFu); }
