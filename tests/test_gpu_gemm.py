@@ -71,8 +71,11 @@ def test_gemm_gelu_mx_epilogue(pkg, dev):
     np.testing.assert_array_equal(inter_mx.codes.view(torch.uint8).cpu().numpy(), codes)
 
 
-def test_gemm_gated_residual_epilogue(pkg, dev):
-    M, N, K = 300, 512, 512
+@pytest.mark.parametrize("K", [384, 512])  # the simple loop and the pipelined ring kernel
+def test_gemm_gated_residual_epilogue(pkg, dev, K):
+    """bf16(res + bf16(y) * gate) on every element; M = 300 leaves the second row tile with one
+    partial and three empty 64-row halves (the residual rows past M read as zero)."""
+    M, N = 300, 512
     xq, wq, ops, b = _operands(pkg, dev, M, N, K, seed=23)
     g = torch.Generator().manual_seed(24)
     res = torch.randn(M, N, generator=g).to(torch.bfloat16)

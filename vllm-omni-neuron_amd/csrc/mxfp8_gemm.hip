@@ -318,9 +318,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, int r
 __device__ __forceinline__ void store_rows_nt16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 d) {
   __builtin_amdgcn_raw_buffer_store_b128(u32x4{d.x, d.y, d.z, d.w}, r, (int)off, 0, 2);
 }
-__device__ __forceinline__ uint4 load_rows16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
+
+// The gated-residual epilogue's residual rows of one half (64 tokens x the wave's 128 features,
+// bf16) into the wave's private 16 KiB residual area by direct-to-LDS loads, so that their latency
+// runs under the epilogue's math instead of after it: instruction it lands rows 4 it .. 4 it + 3,
+// lane l row 4 it + (l >> 4), 16-byte chunk l & 15, at byte 1024 it + 16 l -- where lane l reads
+// it back. Rows past M read zero (the resource ends at row M, as the stores' does).
+__device__ __forceinline__ void residual_to_lds(const GemmArgs& g, uint8_t* rarea, int mbase, int nw, int lane) {
+  // the tile's row and column pass through an empty asm so that none of this is computed ahead of
+  // the k loop and held through it (which spilled registers inside the loop)
+  asm volatile("" : "+s"(mbase), "+s"(nw));
+  const int rows = max(0, min(64, (int)g.M - mbase));
+  const uint32_t rb = (uint32_t)g.ldo * 2;
+  // the resource's words through readfirstlane, as in rows_rsrc (the inputs are wave-uniform, which
+  // the compiler does not prove, and the load takes the resource in scalar registers)
+  const uint64_t base = reinterpret_cast<uint64_t>(g.residual + (size_t)mbase * g.ldo + nw);
+  const u32x4 r = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) & 0xFFFFu,
+                   (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)rows * rb), 0x00020000u};
+  const uint32_t voff = (uint32_t)(lane >> 4) * rb + (uint32_t)(lane & 15) * 16;
+#pragma unroll
+  for (int it = 0; it < 16; ++it) lds_dma_b128(r, voff + (uint32_t)(it * 4) * rb, lds_addr(rarea + it * 1024));
 }
 
 // bf16 staging: [64 tokens][256 B], 16-byte chunk index XOR (token & 15) -- the 16 lanes of an LDS
@@ -383,11 +401,14 @@ __device__ __forceinline__ void epi_values(const f32x16& a, const EpiVectors<kSc
 // on the spot.
 template <int EPI, bool kScaled, bool kSumsq>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4], const float* vec, uint8_t* stage,
-                                         int m0, int n0, int wm, int wn) {
+                                         int m0, int n0, int wm, int wn, uint8_t* rarea = nullptr) {
 #pragma clang fp contract(off)
   const int lane = fresh_lane_id();
   const int h = lane >> 5, r32 = lane & 31;
   const int nw = n0 + wn * 128;  // first feature of the wave's block
+  // gated residual: `rarea` is 16 KiB of LDS private to the wave that no load targets during the
+  // epilogue; the first half's residual rows go there now, the second half's once the first's are read
+  if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) residual_to_lds(g, rarea, m0 + wm * 128, nw, lane);
   EpiVectors<kScaled> ev;
   load_epi_vectors<kScaled>(vec, wn, h, ev);
 #pragma unroll
@@ -479,7 +500,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
     // complete before the first store: vmcnt counts loads and stores together and stores may finish
     // out of order with loads, so once stores are queued between them and the next tile's stage-1
     // loads, the partial vmcnt wait at the top of the tile would no longer certify stage 0.
-    if (hf == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // The gated residual waits here for its half's residual rows too (the second half's were issued
+    // before the first half's stores, so only a full wait certifies them).
+    if (hf == 0 || EPI == WANMI_EPI_GATED_RESIDUAL) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     if constexpr (EPI == WANMI_EPI_GELU_MX) {
       const uint32_t rb = (uint32_t)g.ldo;  // bytes per output row
       const auto orsrc = rows_rsrc(reinterpret_cast<uint8_t*>(g.out) + (size_t)mbase * rb + nw, rows, rb);
@@ -491,15 +514,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       for (int it = 0; it < 8; ++it)
         store_rows_nt16(orsrc, (uint32_t)(it * 8 + (lane >> 3)) * rb + (uint32_t)chunk * 16, d[it]);
     } else if constexpr (EPI == WANMI_EPI_GATED_RESIDUAL) {
-      // out = bf16(res + bf16(v) * gate), 8 features per lane; the residual is read coalesced too
+      // out = bf16(res + bf16(v) * gate), 8 features per lane; the residual rows come from the
+      // wave's residual area, where lane l's 16 bytes of row 4 it + (l >> 4) sit at 1024 it + 16 l
       const uint32_t rb = (uint32_t)g.ldo * 2;
-      const auto rrsrc = rows_rsrc(g.residual + (size_t)mbase * g.ldo + nw, rows, rb);
       const auto orsrc = rows_rsrc(reinterpret_cast<uint16_t*>(g.out) + (size_t)mbase * g.ldo + nw, rows, rb);
       const int chunk = lane & 15;
-      uint4 res[16];
-#pragma unroll
-      for (int it = 0; it < 16; ++it)
-        res[it] = load_rows16(rrsrc, (uint32_t)(it * 4 + (lane >> 4)) * rb + (uint32_t)chunk * 16);
       const float4 g0 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8);
       const float4 g1 = *reinterpret_cast<const float4*>(vec + 512 + wn * 128 + chunk * 8 + 4);
       const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
@@ -507,8 +526,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       for (int it = 0; it < 16; ++it) {
         const int tok = it * 4 + (lane >> 4);
         const uint4 d = *reinterpret_cast<const uint4*>(stage + stg16(tok, chunk));
+        const uint4 rs = *reinterpret_cast<const uint4*>(rarea + it * 1024 + lane * 16);
         const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-        const uint32_t rv[4] = {res[it].x, res[it].y, res[it].z, res[it].w};
+        const uint32_t rv[4] = {rs.x, rs.y, rs.z, rs.w};
         uint32_t o[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -517,6 +537,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
           o[k] = pack_bf16x2(y0, y1);
         }
         store_rows_nt16(orsrc, (uint32_t)tok * rb + (uint32_t)chunk * 16, make_uint4(o[0], o[1], o[2], o[3]));
+      }
+      if (hf == 0) {
+        // every read of the area is complete before the second half's rows may land in it
+        __builtin_amdgcn_s_waitcnt(waitcnt_lgkm(0));
+        residual_to_lds(g, rarea, mbase + 64, nw, lane);
       }
     } else {
       const uint32_t rb = (uint32_t)g.ldo * 2;
@@ -700,6 +725,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
     if (kPrefetchBeforeEpilogue && has_next) prefetch0(tile_loads(g, vn), svec[vb ^ 1]);
     {
       uint8_t* stage = smem1 + wave * kStageWave;
+      // the gated residual's rows: smem0, which that epilogue's tile only prefetches into after it
+      uint8_t* rarea = smem0 + wave * kStageWave;
       const bool scaled = g.row_scale || g.col_scale;
       if constexpr (EPI == kEpiVt) {
         if (scaled) epilogue_vt<true>(g, acc, svec[vb], stage, m0, n0, wm, wn);
@@ -713,8 +740,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_kernel(GemmArgs g) {
           else epilogue<EPI, false, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
         }
       } else {
-        if (scaled) epilogue<EPI, true, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
-        else epilogue<EPI, false, false>(g, acc, svec[vb], stage, m0, n0, wm, wn);
+        if (scaled) epilogue<EPI, true, false>(g, acc, svec[vb], stage, m0, n0, wm, wn, rarea);
+        else epilogue<EPI, false, false>(g, acc, svec[vb], stage, m0, n0, wm, wn, rarea);
       }
     }
     if (!has_next) break;
@@ -967,6 +994,9 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_ring_kernel(GemmArgs g) {
     if (kPrefetchBeforeEpilogue && has_next) prefetch0(tile_loads(g, vn), par_n);
     {
       uint8_t* stage = wave < 2 ? sAct[1] + wave * kStageWave : sWh[wave];
+      // the gated residual's rows: activation slot 0 and half slots 0-1, which that epilogue's tile
+      // only prefetches into after it
+      uint8_t* rarea = wave < 2 ? sAct[0] + wave * kStageWave : sWh[wave - 2];
       const bool scaled = g.row_scale || g.col_scale;
       if constexpr (EPI == kEpiVt) {
         if (scaled) epilogue_vt<true>(g, acc, vec, stage, m0, n0, wm, wn);
@@ -980,8 +1010,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_ring_kernel(GemmArgs g) {
           else epilogue<EPI, false, false>(g, acc, vec, stage, m0, n0, wm, wn);
         }
       } else {
-        if (scaled) epilogue<EPI, true, false>(g, acc, vec, stage, m0, n0, wm, wn);
-        else epilogue<EPI, false, false>(g, acc, vec, stage, m0, n0, wm, wn);
+        if (scaled) epilogue<EPI, true, false>(g, acc, vec, stage, m0, n0, wm, wn, rarea);
+        else epilogue<EPI, false, false>(g, acc, vec, stage, m0, n0, wm, wn, rarea);
       }
     }
     if (!has_next) break;
