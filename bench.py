@@ -6,14 +6,16 @@ attention, one CFG branch, cross-attention K/V cached (projected once before tim
 reference does per generation), the RoPE tables built inside every timed forward (as the reference
 builds them per forward). After the metric the same 40 blocks are timed through the reference's own
 FP8 recipe (ROW activations, drop-ins composed as its modules call them; ``row_recipe``) and the
-40-block forward is measured at 720p (21x45x80 = 75600 tokens; ``p720``). Random N(0, 0.02) weights (q/k RMSNorm gammas N(1, 0.02)),
-seeded N(0, 1) latent tokens, text context and timestep modulation -- synthetic data.
+40-block forward is measured at 720p (21x45x80 = 75600 tokens; ``p720``). Random N(0, 0.02)
+weights (q/k RMSNorm gammas N(1, 0.02)), seeded N(0, 1) latent tokens, text context and timestep
+modulation -- synthetic data.
 
 Prints one JSON line. ``value`` is milliseconds per DiT step (lower is better). The roofline entry
 is the dominant kernel (self-attention), timed by HIP events around each of its launches inside the
 timed steps; the other kernels' times come from events around every launch of one more forward
-after the timed steps (events around every launch would add about 2.5 ms to the step). The CPU baseline is the reference's BF16 eager block (restated
-in the oracle) timed on this host's cores at the 1560-token block shape, extrapolated to the step.
+after the timed steps (events around every launch would add about 2.5 ms to the step). The CPU
+baseline is the reference's BF16 eager block (restated in the oracle) timed on this host's cores at
+the 1560-token block shape, extrapolated to the step.
 """
 
 from __future__ import annotations
