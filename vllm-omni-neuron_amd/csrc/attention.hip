@@ -1153,7 +1153,9 @@ extern "C" int wanmi_attention_const_max_qrr(const void* q, int64_t q_head_strid
                                              const float* q_sin, void* stream) {
   using namespace wanmi;
   clear_error();
-  WANMI_REQUIRE(q_rr && q_gamma, WANMI_ERR_ARG, "wanmi_attention_const_max_qrr: q_rr and q_gamma are required");
+  // (no queries: an empty q_rr may have no storage)
+  WANMI_REQUIRE((Sq == 0 || q_rr) && q_gamma, WANMI_ERR_ARG,
+                "wanmi_attention_const_max_qrr: q_rr and q_gamma are required");
   WANMI_REQUIRE((q_cos == nullptr) == (q_sin == nullptr), WANMI_ERR_ARG,
                 "wanmi_attention_const_max_qrr: q_cos and q_sin must both be given or both be null");
   WANMI_REQUIRE(((uintptr_t)q_rr % 4) == 0 && ((uintptr_t)q_gamma % 16) == 0 &&
@@ -1179,7 +1181,9 @@ extern "C" int wanmi_attention_const_max_qprep(const void* q, int64_t q_head_str
                                                const float* q_cos, const float* q_sin, float q_eps, void* stream) {
   using namespace wanmi;
   clear_error();
-  WANMI_REQUIRE(q_sumsq && q_gamma, WANMI_ERR_ARG, "wanmi_attention_const_max_qprep: q_sumsq and q_gamma are required");
+  // (no queries: an empty q_sumsq may have no storage)
+  WANMI_REQUIRE((Sq == 0 || q_sumsq) && q_gamma, WANMI_ERR_ARG,
+                "wanmi_attention_const_max_qprep: q_sumsq and q_gamma are required");
   WANMI_REQUIRE((q_cos == nullptr) == (q_sin == nullptr), WANMI_ERR_ARG,
                 "wanmi_attention_const_max_qprep: q_cos and q_sin must both be given or both be null");
   WANMI_REQUIRE(heads % 4 == 0 && q_sumsq_ld >= heads && q_sumsq_ld % 4 == 0, WANMI_ERR_ARG,
@@ -1244,7 +1248,7 @@ extern "C" int wanmi_attention_exact(const void* q, int64_t q_head_stride, int64
   clear_error();
   WANMI_REQUIRE(out_mode == WANMI_ATTN_OUT_TOKEN || out_mode == WANMI_ATTN_OUT_DMAJOR, WANMI_ERR_ARG,
                 "wanmi_attention_exact: out_mode %d must be token-major or d-major bf16", out_mode);
-  WANMI_REQUIRE(row_sum && ((uintptr_t)row_sum % 4) == 0, WANMI_ERR_ARG,
+  WANMI_REQUIRE((Sq == 0 || row_sum) && ((uintptr_t)row_sum % 4) == 0, WANMI_ERR_ARG,
                 "wanmi_attention_exact: row_sum must be a 4-byte aligned [heads][Sq] buffer");
   WANMI_REQUIRE(out_mode != WANMI_ATTN_OUT_TOKEN || (((uintptr_t)out % 4) == 0 && o_head_stride % 2 == 0 &&
                                                      o_token_stride % 2 == 0),

@@ -1149,7 +1149,8 @@ extern "C" int wanmi_mxfp8_gemm_rowsumsq(const uint8_t* a_codes, const uint8_t* 
                                          int64_t ldo, float* row_sumsq, int64_t sumsq_cols, void* stream) {
   using namespace wanmi;
   clear_error();
-  WANMI_REQUIRE(row_sumsq && ((uintptr_t)row_sumsq % 4) == 0, WANMI_ERR_ARG,
+  // no rows: nothing is written, and an empty row_sumsq may have no storage
+  WANMI_REQUIRE(M == 0 || (row_sumsq && ((uintptr_t)row_sumsq % 4) == 0), WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm_rowsumsq: row_sumsq must be a 4-byte aligned pointer");
   WANMI_REQUIRE(sumsq_cols >= 0 && sumsq_cols <= N && sumsq_cols % 128 == 0, WANMI_ERR_ARG,
                 "wanmi_mxfp8_gemm_rowsumsq: sumsq_cols=%lld must be a multiple of 128 in [0, N]", (long long)sumsq_cols);

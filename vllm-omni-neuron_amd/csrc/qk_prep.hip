@@ -408,7 +408,7 @@ extern "C" int wanmi_qk_rmsnorm_rope_to(const void* x, int64_t S, int64_t ld, in
                                         void* out, int64_t out_token_stride, int64_t out_head_stride, void* stream) {
   using namespace wanmi;
   clear_error();
-  WANMI_REQUIRE(out && ((uintptr_t)out % 16) == 0 && out_token_stride % 8 == 0 && out_head_stride % 8 == 0 &&
+  WANMI_REQUIRE((S == 0 || out) && ((uintptr_t)out % 16) == 0 && out_token_stride % 8 == 0 && out_head_stride % 8 == 0 &&
                     out_token_stride >= 0 && out_head_stride >= 0,
                 WANMI_ERR_ARG,
                 "wanmi_qk_rmsnorm_rope_to: out must be 16-byte aligned with strides that are multiples of 8 elements");
@@ -424,8 +424,9 @@ extern "C" int wanmi_qk_rmsnorm_rope_qrr(void* x, int64_t S, int64_t ld, int hea
                                          float q_eps, float* q_rr, void* stream) {
   using namespace wanmi;
   clear_error();
-  WANMI_REQUIRE(q_sumsq && q_rr && ((uintptr_t)q_sumsq % 4) == 0 && ((uintptr_t)q_rr % 4) == 0, WANMI_ERR_ARG,
-                "wanmi_qk_rmsnorm_rope_qrr: q_sumsq and q_rr must be 4-byte aligned pointers");
+  // no tokens: nothing is read or written, and empty q_sumsq / q_rr may have no storage
+  WANMI_REQUIRE(S == 0 || (q_sumsq && q_rr && ((uintptr_t)q_sumsq % 4) == 0 && ((uintptr_t)q_rr % 4) == 0),
+                WANMI_ERR_ARG, "wanmi_qk_rmsnorm_rope_qrr: q_sumsq and q_rr must be 4-byte aligned pointers");
   WANMI_REQUIRE(q_heads > 0 && q_sumsq_ld >= q_heads, WANMI_ERR_ARG,
                 "wanmi_qk_rmsnorm_rope_qrr: need q_heads > 0 and q_sumsq_ld >= q_heads (q_heads=%d, ld=%lld)", q_heads,
                 (long long)q_sumsq_ld);
