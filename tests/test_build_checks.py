@@ -76,3 +76,23 @@ def test_store_data_hazard_cleared_by_wait_states_or_other_registers():
     # 64-bit stores are not affected
     asm = _asm("buffer_store_dwordx2 v[48:49], v63, s[36:39], 0 offen", "v_mov_b32_e32 v48, 0")
     assert build.store_data_hazards(asm) == []
+
+
+def test_store_data_hazard_follows_branches():
+    """The wait states after a wide store are counted along each path control can take: past an
+    unconditional branch the text that follows is another block, and a conditional branch leads both
+    to its target and to the next instruction."""
+    store = "buffer_store_dwordx4 v[0:3], v9, s[0:3], 0 offen"
+    # the next block in the text is not a successor; the target starts with two scalar instructions
+    asm = _asm(store, "s_branch .LBB0_2", ".LBB0_1:", "v_mov_b32_e32 v1, 0", ".LBB0_2:", "s_mov_b32 s0, 0",
+               "s_mov_b32 s1, 0", "v_mov_b32_e32 v1, 0")
+    assert build.store_data_hazards(asm) == []
+    # ... but a write right at the target is found
+    asm = _asm(store, "s_branch .LBB0_2", ".LBB0_1:", "s_nop 7", ".LBB0_2:", "v_mov_b32_e32 v2, 0")
+    assert len(build.store_data_hazards(asm)) == 1
+    # a conditional branch: the target path and the fall-through path are both checked
+    asm = _asm(store, "s_cbranch_scc1 .LBB0_2", "s_mov_b32 s0, 0", "s_mov_b32 s0, 0", ".LBB0_2:",
+               "v_mov_b32_e32 v2, 0")
+    assert len(build.store_data_hazards(asm)) == 1
+    asm = _asm(store, "s_cbranch_scc1 .LBB0_2", "v_mov_b32_e32 v3, 0", "s_endpgm", ".LBB0_2:", "s_nop 3")
+    assert len(build.store_data_hazards(asm)) == 1

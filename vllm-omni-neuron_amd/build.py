@@ -108,6 +108,40 @@ def store_data_hazards(asm: str, window: int = 2) -> list[str]:
     missed this (an adaLN store followed directly by a move into one of its data registers), so
     every kernel's generated code is checked."""
     lines = [ln.split(";")[0].strip() for ln in asm.splitlines()]
+    labels = {ln[:-1]: k for k, ln in enumerate(lines) if ln.endswith(":") and not ln.startswith(".")
+              or ln.startswith(".LBB") and ln.endswith(":")}
+
+    def scan(j: int, states: int, data: set, store: str, found: list, seen: set) -> None:
+        # every instruction that may execute within `window` wait states of the store, along each
+        # control-flow path: an unconditional branch continues at its target, a conditional one at
+        # both its target and the next instruction
+        while states < window and j < len(lines):
+            if (j, states) in seen:
+                return
+            seen.add((j, states))
+            nxt = lines[j]
+            j += 1
+            if not nxt or nxt.startswith((".", "#")) and not nxt.endswith(":") or nxt.endswith(":"):
+                continue
+            nop = nxt.split()[0]
+            if nop == "s_nop":
+                states += int(nxt.split()[1], 0) + 1
+                continue
+            if nop.startswith("v_") and _vgprs(nxt[len(nop):].split(",")[0]) & data:
+                found.append(f"{store}  (then {nxt}, {states} wait states)")
+                return
+            if nop in ("s_endpgm", "s_setpc_b64"):
+                return
+            if nop == "s_branch" or nop.startswith("s_cbranch"):
+                target = labels.get(nxt.split()[1])
+                if target is None:  # an unknown target: assume the worst (keep scanning linearly)
+                    states += 1
+                    continue
+                scan(target + 1, states + 1, data, store, found, seen)
+                if nop == "s_branch":
+                    return
+            states += 1
+
     found = []
     for i, ln in enumerate(lines):
         op = ln.split()[0] if ln else ""
@@ -117,20 +151,9 @@ def store_data_hazards(asm: str, window: int = 2) -> list[str]:
             continue
         operands = [o.strip() for o in ln[len(op):].split(",")]
         data = _vgprs(operands[0] if op.startswith("buffer") else operands[1])
-        states, j = 0, i + 1
-        while states < window and j < len(lines):
-            nxt = lines[j]
-            j += 1
-            if not nxt or nxt.startswith((".", "#")) or nxt.endswith(":"):
-                continue
-            nop = nxt.split()[0]
-            if nop == "s_nop":
-                states += int(nxt.split()[1], 0) + 1
-                continue
-            if nop.startswith("v_") and _vgprs(nxt[len(nop):].split(",")[0]) & data:
-                found.append(f"{ln}  (then {nxt}, {states} wait states)")
-                break
-            states += 1
+        hits: list = []
+        scan(i + 1, 0, data, ln, hits, set())
+        found.extend(hits[:1])
     return found
 
 
