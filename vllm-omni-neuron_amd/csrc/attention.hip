@@ -572,12 +572,47 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
   issue_tile(0, 2);
 
   const int64_t qvalid = a.Sq - q0 < 32 ? (a.Sq - q0 > 0 ? a.Sq - q0 : 0) : 32;
+  // The wave's 32 query rows of head hd, 256 bytes each. Load t covers rows 8 (t & 3) .. + 7, the
+  // 128-byte half t >> 2 of each (lane l: row 8 (t & 3) + (l >> 3), 16-byte chunk l & 7), so one
+  // instruction touches eight cache lines; gathered straight into the MFMA's lane layout (lane l
+  // holds query l & 31) each touched 32, and those gathers cost the kernel 11%. rearrange_q below
+  // moves the rows into the lane layout through LDS.
   auto issue_q = [&](int hd, u32x4 (&qv)[8]) {
     const __amdgpu_buffer_rsrc_t r_q = attn_rsrc(a.q + hd * a.q_hs + (qvalid > 0 ? q0 * a.q_ss : 0),
                                                  qvalid > 0 ? ((qvalid - 1) * a.q_ss + 128) * 2 : 0);
+    // the lane's part of the offset in one register, recomputed per call (held across the head
+    // loop, eight per-lane offsets were spilled and their reloads waited for the K/V loads in
+    // flight); the row group and half as the scalar offset
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    const uint32_t voff = (uint32_t)(((l >> 3) * a.q_ss + 8 * (l & 7)) * 2);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-      qv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_q, (uint32_t)((col * a.q_ss + 16 * t + 8 * hq) * 2), 0, 0);
+      qv[t] = __builtin_amdgcn_raw_buffer_load_b128(r_q, voff, (uint32_t)((8 * (t & 3) * a.q_ss + 64 * (t >> 2)) * 2), 0);
+  };
+  // The loaded rows into the B-operand layout of the QK^T MFMAs: qv[t] = the 16 bytes of row
+  // `col`, k-step t, half hq (row bytes 32 t + 16 hq). One 128-byte half of all 32 rows at a time
+  // goes through `qs`, 4 KiB of LDS private to the wave, held as [row][8 chunks] with chunk
+  // c ^ ((row >> 1) & 7), which keeps both the writes (two rows of eight chunks per 16 lanes) and the
+  // reads (sixteen rows of one chunk) free of bank conflicts. A wave's LDS operations complete in
+  // order, so the second half's writes cannot overtake the first half's reads.
+  auto rearrange_q = [&](uint8_t* qs, u32x4 (&qv)[8]) {
+    int l = lane;
+    asm volatile("" : "+v"(l));  // addresses from the lane id per call, as in issue_q
+    // write t: row 8 t + (l >> 3), chunk l & 7, whose swizzle (row >> 1) & 7 = 4 (t & 1) | (l >> 4)
+    const int wsw = (l & 7) ^ (l >> 4);
+    uint8_t* w0 = qs + (l >> 3) * 128 + (wsw << 4);
+    uint8_t* w1 = qs + (l >> 3) * 128 + ((wsw ^ 4) << 4);
+    // read t: row l & 31, chunk 2 t + (l >> 5)
+    const uint8_t* rb = qs + (l & 31) * 128;
+    const int rsw = ((l & 31) >> 1) & 7, h = l >> 5;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) *reinterpret_cast<u32x4*>((t & 1 ? w1 : w0) + t * 1024) = qv[4 * hf + t];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) qv[4 * hf + t] = *reinterpret_cast<const u32x4*>(rb + ((((2 * t) | h) ^ rsw) << 4));
+    }
   };
   const bool qprep = a.q_sumsq != nullptr || a.q_rr != nullptr;
   auto issue_gamma = [&](int hd) {
@@ -635,6 +670,13 @@ __global__ __launch_bounds__(kThreads) void attention_head_group_kernel(AttnArgs
     // This head's Q and gamma are in once every outstanding load is (tiles g0 and g0 + 1 were
     // issued before them).
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // Q through the wave's MX staging area (free here: the previous head's staging was read back
+    // above, in this wave's LDS order). Waves 0-3 use the K half of a ring slot that no load in
+    // flight targets and that no wave reads until this head's first barrier: slot 3 in the first
+    // head (tiles 0-2 are in slots 0-2, tile 3 goes out after the barrier of tile 1); later, the slot
+    // of tile g0 + 2 (tile g0 - 2's K was read before the barrier of tile g0 - 1; tile g0 + 2 is
+    // issued after this head's first barrier).
+    rearrange_q(wave < 4 ? sK[hl == 0 ? kStages - 1 : (g0 + 2) % kStages] + wave * 4096 : sStg[wave & 3], qv);
     if (qprep) {
       const float4* gl = reinterpret_cast<const float4*>(sgam[wave]);
 #pragma unroll
