@@ -34,10 +34,12 @@ def _check_attn(out, ref):
 
 # key counts cover 1, 2, 3, 4, 5, 7 and 8 tiles of 64 (the K/V ring loads two tiles per barrier, so
 # odd and even tile counts and a partial last tile take different paths). With 3 to 16 tiles and
-# more than one head, a workgroup walks several heads (2, 3, 4 or 5 per group here, the last two with
-# several groups: 12 heads in three groups of 4 over a last tile of one key, 10 in two of 5). With
-# the heads a multiple of 8 the one-head-per-workgroup kernels place whole heads per XCD: 8 heads
-# over 2 tiles (the short-key kernel) and 16 over 18 tiles.
+# more than one head, a workgroup walks several heads (grids this small fit one round of the CUs,
+# where two heads per group leave the most workgroups: 2 and 4 heads in groups of 2, 12 heads in six
+# over a last tile of one key, 10 in five; 3 heads in one group of 3; larger groups in
+# test_cross_attention_head_groups). With the heads a multiple of 8 the one-head-per-workgroup
+# kernels place whole heads per XCD: 8 heads over 2 tiles (the short-key kernel) and 16 over 18
+# tiles.
 @pytest.mark.parametrize("Sq,Sk,N", [(1, 1, 1), (300, 200, 2), (129, 197, 3), (64, 512, 4), (96, 100, 2),
                                      (70, 150, 1), (40, 300, 1), (33, 448, 1), (1000, 129, 12), (513, 512, 10),
                                      (300, 100, 8), (200, 1100, 16)])
@@ -225,6 +227,39 @@ def test_cross_attention_full_shape_rows(pkg, dev):
     for h in (0, 21, 39):
         ref = oa.torch_attend(q[rows, h].cpu(), k[:, h].cpu(), v[:, h].cpu(), 128**-0.5, dtype=torch.float64)
         _check_attn(out.view(S, N, 128)[rows, h].cpu(), ref)
+
+
+@pytest.mark.parametrize("Sq,N,hpw", [(16384, 12, 3), (16384, 20, 5), (32760, 8, 4)])
+def test_cross_attention_head_groups(pkg, dev, Sq, N, hpw):
+    """Head groups of 3, 4 and 5 over many workgroups (64 query blocks x 4 groups of 3 heads or
+    4 x 5, 128 blocks x 2 groups of 4: one round of 256 CUs each), 512 keys: sampled query rows of
+    every head group against exact fp64 attention, the d-major output equal to the token-major one
+    and the MX output the MX quantization of it, bit for bit. The expected group size is the
+    library's choice for an MI355X (256 CUs); on another CU count the same checks run at its
+    choice."""
+    ops = pkg.attention_ops
+    Sk = 512
+    g = torch.Generator().manual_seed(Sq + N)
+    q = torch.randn(Sq, N, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(Sk, N, 128, generator=g).to(torch.bfloat16)
+    s = 128**-0.5
+    vt, _ = ops.transpose_heads(v.to(dev))
+    kmax = ops.head_max_norm(k.to(dev))
+    tok = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_TOKEN)
+    dm = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_DMAJOR)
+    mx = ops.attention_core(q.to(dev), k.to(dev), vt, kmax, s, ops.OUT_MX)
+    tok = tok.cpu().view(Sq, N, 128)
+    assert torch.equal(dm.cpu().permute(0, 2, 1).contiguous(), tok.permute(1, 0, 2).contiguous())
+    codes, scales = omx.mx_quantize(tok.view(Sq, N * 128).float().numpy())
+    np.testing.assert_array_equal(mx.codes.view(torch.uint8).cpu().numpy(), codes)
+    np.testing.assert_array_equal(mx.scales.cpu().numpy(), scales)
+    rows = torch.cat([torch.arange(0, 32), torch.randint(0, Sq, (32,), generator=g), torch.arange(Sq - 32, Sq)])
+    for h0 in range(0, N, hpw):  # the first and last head of every group
+        for h in sorted({h0, h0 + hpw - 1}):
+            ref = oa.torch_attend(q[rows, h].unsqueeze(0), k[:, h].unsqueeze(0), v[:, h].unsqueeze(0), s,
+                                  dtype=torch.float64)
+            _check_attn(tok[rows, h].unsqueeze(0), ref)
 
 
 @pytest.mark.parametrize("with_rope", [True, False])

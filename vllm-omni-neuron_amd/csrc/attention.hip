@@ -31,10 +31,28 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int BKV = 64;            // keys per LDS tile (two 32-key halves)
 constexpr int kStages = 4;         // LDS ring depth in tiles
 constexpr float kSumFloor = 1e-37f;
-#ifndef WANMI_CROSS_HEADS_PER_GROUP
-#define WANMI_CROSS_HEADS_PER_GROUP 5
-#endif
-constexpr int kCrossHeadsPerGroup = WANMI_CROSS_HEADS_PER_GROUP;  // heads per workgroup, short key sequences
+constexpr int kCrossHeadsPerGroupMax = 20;  // heads per workgroup, short key sequences (upper bound)
+
+// Heads per workgroup of attention_head_group_kernel: the divisor c >= 2 of `heads` (at most
+// kCrossHeadsPerGroupMax) whose grid of blocks * heads / c workgroups finishes first when every CU
+// takes one at a time, each costing c heads plus a fixed part (the first three key tiles, the
+// queries' norm sum, the last head's drain) of about 0.3 head, measured at 32760 queries over 512
+// keys: 389.4 / 379.9 / 371.8 us with 5 / 10 / 20 heads per workgroup, 4 / 2 / 1 rounds of 256.
+// The larger group wins a tie. 20 heads at 32760 queries (128 blocks), 8 at 75600 (296 blocks).
+inline int cross_heads_per_group(int64_t blocks, int heads, int cus) {
+  int best_c = 1;
+  int64_t best = INT64_MAX;
+  for (int c = 2; c <= kCrossHeadsPerGroupMax && c <= heads; ++c) {
+    if (heads % c) continue;
+    const int64_t wgs = blocks * (heads / c);
+    const int64_t cost = ((wgs + cus - 1) / cus) * (10 * c + 3);
+    if (cost <= best) {
+      best = cost;
+      best_c = c;
+    }
+  }
+  return best_c;
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kAttnRsrcWord3);
@@ -1149,11 +1167,12 @@ static int attention_impl(const void* q, int64_t q_head_stride, int64_t q_token_
   const dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)heads);
   const bool rebase_k = ((Sk - 1) * k_token_stride + 128) * 2 >= (1LL << 31);
   // Short key sequences of three tiles or more with queries that take no RoPE (cross-attention):
-  // up to kCrossHeadsPerGroup heads per workgroup (the largest divisor of `heads` not above it).
+  // several heads per workgroup (cross_heads_per_group; one head per workgroup when `heads` has no
+  // divisor from 2 up).
   int hpw = 1;
   if (Sk <= 1024 && Sk > 2 * BKV && qp.cos == nullptr && !rebase_k) {
-    hpw = kCrossHeadsPerGroup < heads ? kCrossHeadsPerGroup : heads;
-    while (heads % hpw) --hpw;
+    const int cus = device_cu_count();
+    hpw = cross_heads_per_group((int64_t)grid.x, heads, cus > 0 ? cus : 256);
   }
   a.heads_per_group = hpw;
   if (hpw > 1)
